@@ -1,0 +1,144 @@
+/*
+ * scree_hip.h -- C ABI of the MI355X (gfx950) varlen kernel library
+ * (libscree_hip.so).
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  Every tensor is caller-owned device
+ *     memory; the library never allocates.  Scratch memory is passed in as a
+ *     `workspace` whose size the matching *_workspace_bytes() call reports.
+ *   - `stream` is a hipStream_t passed as void* (NULL = legacy default
+ *     stream).  All work is enqueued on it; no call synchronises the host.
+ *   - Return value: SCREE_OK (0) or a negative SCREE_ERR_* code.  Arguments
+ *     are validated on the host before anything is launched;
+ *     scree_last_error() returns a message for the calling thread's last
+ *     failure.
+ *   - dtype codes: SCREE_DTYPE_F32 / F16 / BF16.  Attention takes F16 or
+ *     BF16 (as the reference's GPU launcher asserts,
+ *     src/scree/kernels/triton/varlen_attention.py:213-215); the norms take
+ *     all three.
+ *   - `cu_seqlens` is the int32 offsets vector of length batch+1 (the
+ *     scree.Array `offsets`, src/scree/_core.py:22-62), resident on the
+ *     device.  It is read only by device code: no call copies it to the host.
+ *
+ * Layouts
+ *   - Attention tensors are (total_tokens, heads, head_dim) with the
+ *     head_dim axis contiguous; row and head strides are given in elements
+ *     and must keep every row 16-byte aligned.  lse and delta are contiguous
+ *     (total_tokens, heads) fp32.
+ *   - Norm tensors are contiguous (rows, dim); rstd / mean are (rows) fp32.
+ */
+#ifndef SCREE_HIP_H
+#define SCREE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SCREE_ABI_VERSION 1
+
+enum {
+  SCREE_DTYPE_F32 = 0,
+  SCREE_DTYPE_F16 = 1,
+  SCREE_DTYPE_BF16 = 2
+};
+
+enum {
+  SCREE_OK = 0,
+  SCREE_ERR_INVALID = -1,     /* bad pointer, size, stride or alignment   */
+  SCREE_ERR_UNSUPPORTED = -2, /* dtype / head_dim this build does not do  */
+  SCREE_ERR_WORKSPACE = -3,   /* workspace missing or too small           */
+  SCREE_ERR_HIP = -4          /* the HIP runtime reported a launch error  */
+};
+
+/* Library ABI version (SCREE_ABI_VERSION of the build). */
+int scree_abi_version(void);
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char* scree_last_error(void);
+
+/* ---------------------------------------------------------------- attention
+ * Replaces the Triton launchers
+ *   varlen_attention_triton           src/scree/kernels/triton/varlen_attention.py:165-268
+ *   varlen_attention_triton_backward  src/scree/kernels/triton/_backward.py:288-396
+ * and the padded (batch, cdiv(max_seq, 64), heads) grid plus the host
+ * `.item()` sync on max_seq they use (varlen_attention.py:220-236,
+ * _backward.py:320-321).
+ */
+
+/* Bytes of workspace scree_attn_schedule needs for `batch` sequences holding
+ * `total_tokens` tokens in all (independent of heads and causality). */
+size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim);
+
+/* Build the longest-work-first tile list for `cu_seqlens` into `workspace`.
+ * Must precede scree_attn_fwd / scree_attn_bwd with the same cu_seqlens,
+ * head_dim and causal flag; the workspace may then be reused by any number of
+ * forward and backward calls.  No counterpart in the reference (its grid is
+ * padded, src/scree/kernels/triton/varlen_attention.py:236). */
+int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                        int head_dim, int causal, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Forward: o = softmax(scale * q k^T [causal-masked]) v per sequence and
+ * lse = natural-log logsumexp of the scaled scores per (token, head).
+ * strides[8] = {q_row, q_head, k_row, k_head, v_row, v_head, o_row, o_head}.
+ * Replaces _varlen_attn_fwd_kernel + launcher
+ * (src/scree/kernels/triton/varlen_attention.py:35-268). */
+int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                   const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                   int head_dim, const int64_t* strides, float softmax_scale, int causal,
+                   int dtype, const void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward: dq, dk, dv from dout, the forward's inputs, its output o and lse.
+ * delta (total_tokens, heads) fp32 receives rowsum(o * dout).
+ * strides[16] = {dout, q, k, v, o, dq, dk, dv} x {row, head}.
+ * Replaces _varlen_attn_bwd_{preprocess,dkv,dq}_kernel + launcher
+ * (src/scree/kernels/triton/_backward.py:36-396). */
+int scree_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
+                   const void* o, const float* lse, void* dq, void* dk, void* dv, float* delta,
+                   const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                   int head_dim, const int64_t* strides, float softmax_scale, int causal,
+                   int dtype, const void* workspace, size_t workspace_bytes, void* stream);
+
+/* -------------------------------------------------------------------- norms
+ * Replace varlen_rmsnorm_triton (src/scree/kernels/triton/varlen_rmsnorm.py:17-99)
+ * and varlen_layernorm_triton (src/scree/kernels/triton/varlen_layernorm.py:14-109).
+ * `weight` / `bias` may be NULL; when given they have the activation dtype
+ * (the reference rounds them to it, varlen_rmsnorm.py:79,
+ * varlen_layernorm.py:84,89).  The backward passes have no counterpart in the
+ * reference, which is forward-only.
+ */
+
+/* Bytes of workspace a norm backward needs for a (rows, dim) input. */
+size_t scree_norm_bwd_workspace_bytes(int64_t rows, int64_t dim);
+
+/* y = x / sqrt(mean(x^2) + eps) [* weight]; rstd (may be NULL) = 1/sqrt(mean(x^2)+eps). */
+int scree_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd, int64_t rows,
+                      int64_t dim, float eps, int dtype, void* stream);
+
+/* dx and (if weight != NULL) dweight, stored in `dparam_dtype`, from dy, x,
+ * weight and the forward's rstd. */
+int scree_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const float* rstd,
+                      void* dx, void* dweight, int dparam_dtype, int64_t rows, int64_t dim,
+                      int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* y = (x - mean) / sqrt(var + eps) [* weight] [+ bias] with the population
+ * variance; mean / rstd (may be NULL) receive the row statistics. */
+int scree_layernorm_fwd(const void* x, const void* weight, const void* bias, void* y,
+                        float* mean, float* rstd, int64_t rows, int64_t dim, float eps,
+                        int dtype, void* stream);
+
+/* dx, dweight (if weight != NULL) and dbias (if dbias != NULL), the
+ * parameter gradients stored in `dparam_dtype`. */
+int scree_layernorm_bwd(const void* dy, const void* x, const void* weight, const float* mean,
+                        const float* rstd, void* dx, void* dweight, void* dbias,
+                        int dparam_dtype, int64_t rows, int64_t dim, int dtype,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCREE_HIP_H */

@@ -1,0 +1,35 @@
+"""CPU oracle for the varlen kernel path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, in numpy, the arithmetic of the reference's numpy
+branch (``src/scree/kernels/reference/*.py``) plus the closed-form backward
+passes and the tile schedule the HIP library builds.  It exists to check the
+HIP kernels and to time the CPU baseline.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it; the product path (``scree_amd``) never does and fails loudly when
+its HIP library is missing.
+
+Pinning status of every function (how a plausible mistake would be caught):
+
+* ``core.offsets_from_lengths`` -- closed form ``[0, cumsum]`` int32, checked
+  bit-exact against the reference's test expectations (``tests/test_core.py``)
+  and against ``np.cumsum`` on random lengths.
+* ``attention.attention_fwd`` -- the reference's known-answer tests
+  (per-sequence textbook softmax, causal first row == v0), brute force in
+  fp64 with explicit Python loops on tiny inputs, and
+  ``torch.nn.functional.scaled_dot_product_attention`` per sequence.
+* ``attention.attention_lse`` -- closed form logsumexp, the invariant
+  ``sum_k exp(S - LSE) == 1`` and ``torch.logsumexp``.
+* ``attention.attention_bwd`` -- torch autograd through SDPA on the same
+  inputs and fp64 central finite differences; invariant ``sum_k dS == 0``.
+* ``norms.*_fwd`` -- the reference's known-answer tests, ``F.rms_norm`` /
+  ``F.layer_norm``, unit-RMS and zero-mean/unit-variance properties.
+* ``norms.*_bwd`` -- torch autograd of ``F.rms_norm`` / ``F.layer_norm`` and
+  fp64 finite differences.
+* ``schedule.build_schedule`` -- brute-force enumeration: every (sequence,
+  block) appears exactly once, costs are non-increasing, ties broken by the
+  stated key.
+
+No function is "parity unpinned".
+"""
+
+from . import attention, core, norms, schedule  # noqa: F401

@@ -1,0 +1,916 @@
+// Varlen causal / non-causal self-attention for gfx950: tile scheduler,
+// forward (O + logsumexp) and backward (dQ with Delta, then dK/dV).
+//
+// Layout: q, k, v, o, do, dq, dk, dv are (total_tokens, heads, D) with the D
+// axis contiguous; lse and delta are contiguous (total_tokens, heads) fp32.
+//
+// Work decomposition.  A sequence of length L has nblk = ceil(L / 128) row
+// blocks.  The scheduler kernel writes one (seq, blk) item per row block, in
+// longest-work-first order, into the workspace; every attention kernel is
+// launched with grid = Tmax * heads (Tmax = ceil(N/128) + B bounds the item
+// count on the host, so the host never reads the offsets) and block b takes
+// item b / heads, head b % heads.  Blocks past the real item count return at
+// once.  No padded grid, no host synchronisation.
+//
+// One workgroup = 4 wavefronts; each wavefront owns 32 rows of its item's
+// 128 (queries for the forward and dQ, keys for dK/dV) and runs 32x32x16
+// MFMAs.  MFMA lane layout (see mfma32 in common.h): for a 32x32 product
+// C = A*B with k = 16, lane l (g = l/32, r = l%32) supplies row r of A and
+// column r of B at k = 8g..8g+7, and receives C[8*(i/4) + 4g + i%4][r] in
+// element i.
+//
+// Scores are formed transposed, S^T = K Q^T, so lane r owns one query and
+// the row softmax is in-lane plus one exchange with lane r^32.  Element i of
+// a 32-key tile of S^T then holds key 8*(i/4) + 4g + i%4, and elements
+// 8h..8h+7 are exactly the keys {16h + 4g + 0..3, 16h + 8 + 4g + 0..3}: used
+// as the k = 16 operand of the next MFMA (P^T as B, with V^T read from LDS at
+// the same two 4-key runs as A), P never leaves registers.
+#include <math.h>
+
+#include "common.h"
+
+namespace scree {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;   // 4 wavefronts
+constexpr int kBM = 128;        // rows per item (4 waves x 32)
+constexpr int kBN = 64;         // keys per staged block (forward, dQ)
+constexpr int kMaxBatch = 2048; // sequences the scheduler handles
+constexpr int kMaxClass = 4096; // row blocks per sequence it sorts (longer: natural order)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+// ------------------------------------------------------------ workspace
+// int32 header[4] = {item count T, batch, kBM, causal}, then int4 items[Tmax]
+// = {seq, blk, start, len}.  start/len are the sequence's offsets clamped to
+// [0, total_tokens], so attention kernels never index outside the tensors
+// even for malformed offsets; if those would make T exceed Tmax the
+// scheduler publishes T = 0 (no work) and header[1] = -1.
+constexpr size_t kHeaderBytes = 16;
+
+inline int64_t tmax_for(int batch, int64_t total) { return (total + kBM - 1) / kBM + batch; }
+
+// ------------------------------------------------------------ scheduler
+__device__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int t = __shfl_up(v, d, kWave);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+// In-place exclusive scan of a[0..n) held in LDS by the whole block; returns
+// the total.  Caller synchronises before; this synchronises after.
+__device__ int block_excl_scan(int* a, int n, int* wtot) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int lane = tid & (kWave - 1), wave = tid / kWave, nw = nt / kWave;
+  const int per = (n + nt - 1) / nt;
+  const int beg = min(n, tid * per), end = min(n, beg + per);
+  int local = 0;
+  for (int i = beg; i < end; ++i) local += a[i];
+  const int incl = wave_incl_scan(local);
+  if (lane == kWave - 1) wtot[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int t = lane < nw ? wtot[lane] : 0;
+    t = wave_incl_scan(t);
+    if (lane < nw) wtot[16 + lane] = t;  // inclusive prefix of wave totals
+  }
+  __syncthreads();
+  int run = incl - local + (wave > 0 ? wtot[16 + wave - 1] : 0);
+  for (int i = beg; i < end; ++i) {
+    const int t = a[i];
+    a[i] = run;
+    run += t;
+  }
+  const int total = wtot[16 + nw - 1];
+  __syncthreads();
+  return total;
+}
+
+// One 1024-thread block.  See oracle/schedule.py for the order produced.
+__global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __restrict__ cu,
+                                                             int batch, int total_tokens,
+                                                             int causal, int tmax,
+                                                             int32_t* __restrict__ header,
+                                                             int4* __restrict__ items) {
+  __shared__ int s_start[kMaxBatch];
+  __shared__ int s_len[kMaxBatch];
+  __shared__ int s_nblk[kMaxBatch];
+  __shared__ int s_rank[kMaxBatch];
+  __shared__ int s_sorted_scan[kMaxBatch + 1];
+  __shared__ int s_nat_scan[kMaxBatch + 1];
+  __shared__ int s_cls[kMaxClass + 2];
+  __shared__ int s_wtot[32];
+  __shared__ int s_cmax;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  if (tid == 0) s_cmax = 0;
+  __syncthreads();
+  for (int s = tid; s < batch; s += nt) {
+    const int a = min(max(cu[s], 0), total_tokens);
+    const int b = min(max(cu[s + 1], a), total_tokens);
+    const int len = b - a;
+    const int nb = (len + kBM - 1) / kBM;
+    s_start[s] = a;
+    s_len[s] = len;
+    s_nblk[s] = nb;
+    s_nat_scan[s] = nb;
+    atomicMax(&s_cmax, nb);
+  }
+  __syncthreads();
+  const int cmax = s_cmax;
+  // Rank by (-nblk, seq): the longest sequences first, ties by index.
+  for (int s = tid; s < batch; s += nt) {
+    const int mine = s_nblk[s];
+    int r = 0;
+    for (int t = 0; t < batch; ++t) {
+      const int o = s_nblk[t];
+      r += (o > mine) || (o == mine && t < s);
+    }
+    s_rank[s] = r;
+    s_sorted_scan[r] = mine;
+  }
+  __syncthreads();
+  const int total = block_excl_scan(s_nat_scan, batch, s_wtot);  // natural-order item index base
+  if (tid == 0) s_nat_scan[batch] = total;
+  const bool by_class = causal && cmax <= kMaxClass;
+  if (!causal) {
+    block_excl_scan(s_sorted_scan, batch, s_wtot);
+  } else if (by_class) {
+    // Histogram of nblk, then two suffix passes by one wave:
+    // A(c) = #{s : nblk_s >= c} and offs(c) = sum_{c' > c} A(c').
+    for (int c = tid; c <= cmax + 1; c += nt) s_cls[c] = 0;
+    __syncthreads();
+    for (int s = tid; s < batch; s += nt) {
+      const int nb = s_nblk[s];
+      if (nb > 0) atomicAdd(&s_cls[nb], 1);
+    }
+    __syncthreads();
+    if (tid < kWave) {  // lane l walks c = cmax - per*l downwards
+      const int lane = tid;
+      // Pass 1: A(c) = sum_{v >= c} hist(v), for c = cmax..1 (suffix scan).
+      const int per = (cmax + kWave - 1) / kWave;
+      const int top = cmax - per * lane;
+      const int bot = max(1, top - per + 1);
+      int local = 0;
+      for (int c = top; c >= bot && c >= 1; --c) local += s_cls[c];
+      int incl = wave_incl_scan(local);
+      int run = incl - local;  // sum of hist above this lane's range
+      for (int c = top; c >= bot && c >= 1; --c) {
+        run += s_cls[c];
+        s_cls[c] = run;  // A(c)
+      }
+      // Pass 2: offs(c) = sum_{c' > c} A(c').
+      local = 0;
+      for (int c = top; c >= bot && c >= 1; --c) local += s_cls[c];
+      incl = wave_incl_scan(local);
+      run = incl - local;
+      for (int c = top; c >= bot && c >= 1; --c) {
+        const int a = s_cls[c];
+        s_cls[c] = run;  // offs(c)
+        run += a;
+      }
+    }
+    __syncthreads();
+  }
+  __syncthreads();
+  // Emit: natural item index i -> (seq, blk) by binary search, then place.
+  const bool fits = total <= tmax;
+  for (int i = tid; fits && i < total; i += nt) {
+    int lo = 0, hi = batch - 1;  // find s with nat[s] <= i < nat[s+1]
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_nat_scan[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    const int s = lo;
+    const int b = i - s_nat_scan[s];
+    int p;
+    if (!causal) p = s_sorted_scan[s_rank[s]] + b;
+    else if (by_class) p = s_cls[b + 1] + s_rank[s];
+    else p = i;
+    items[p] = make_int4(s, b, s_start[s], s_len[s]);
+  }
+  if (tid == 0) {
+    header[0] = fits ? total : 0;
+    header[1] = fits ? batch : -1;
+    header[2] = kBM;
+    header[3] = causal;
+  }
+}
+
+// ------------------------------------------------------- tile staging
+// Copies ROWS rows x D columns of a (tokens, heads, D) tensor, rows
+// [row0, row0 + ROWS) of one head, through registers into LDS.  Rows at or
+// past `limit` are zero-filled, so masked work never reads stale data.
+template <typename T, int D, int ROWS>
+struct Stage {
+  static constexpr int CPR = D / 8;                       // 16-byte chunks per row
+  static constexpr int TOTAL = ROWS * CPR;
+  static constexpr int CH = (TOTAL + kThreads - 1) / kThreads;
+  uint4 r[CH];
+
+  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t row_stride, int row0,
+                                       int limit) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = j * kThreads + threadIdx.x;
+      const int row = c / CPR, col = (c % CPR) * 8;
+      r[j] = make_uint4(0, 0, 0, 0);
+      if (c < TOTAL && row0 + row < limit) r[j] = ld16(base + (int64_t)(row0 + row) * row_stride + col);
+    }
+  }
+  // lds[row][col], leading dimension ld (elements)
+  __device__ __forceinline__ void put_rows(T* lds, int ld) const {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = j * kThreads + threadIdx.x;
+      if (c < TOTAL) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        st16(lds + row * ld + col, r[j]);
+      }
+    }
+  }
+  // lds[col][row] (transposed), leading dimension ld (elements)
+  __device__ __forceinline__ void put_cols(T* lds, int ld) const {
+    uint16_t* l16 = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = j * kThreads + threadIdx.x;
+      if (c < TOTAL) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        const uint32_t w[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          l16[(col + e) * ld + row] = (uint16_t)((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+      }
+    }
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ typename VecT<T>::x8 lds_frag16(const T* p) {
+  return *reinterpret_cast<const typename VecT<T>::x8*>(p);
+}
+// Two 4-element runs (p[0..3], p[8..11]) as one 8-element operand.
+template <typename T>
+__device__ __forceinline__ typename VecT<T>::x8 lds_frag_2x4(const T* p) {
+  typedef typename VecT<T>::x4 x4;
+  typedef typename VecT<T>::x8 x8;
+  const x4 a = *reinterpret_cast<const x4*>(p);
+  const x4 b = *reinterpret_cast<const x4*>(p + 8);
+  x8 out;
+  out[0] = a[0]; out[1] = a[1]; out[2] = a[2]; out[3] = a[3];
+  out[4] = b[0]; out[5] = b[1]; out[6] = b[2]; out[7] = b[3];
+  return out;
+}
+template <typename T>
+__device__ __forceinline__ typename VecT<T>::x8 gmem_frag16(const T* p) {
+  return *reinterpret_cast<const typename VecT<T>::x8*>(p);
+}
+// Elements e0..e0+7 of a 16-float accumulator, rounded, as an operand.
+template <typename T>
+__device__ __forceinline__ typename VecT<T>::x8 pack_frag(const f32x16& c, int e0) {
+  typename VecT<T>::x8 out;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) out[j] = (T)c[e0 + j];
+  return out;
+}
+// Store the 16 values of one 32x32 accumulator column-slice: element i is
+// D-index d0 + 8*(i/4) + 4g + i%4 of a row; scaled by `mul`.
+template <typename T>
+__device__ __forceinline__ void store_row_slice(T* row_ptr, int d0, int g, const f32x16& c,
+                                                float mul) {
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    const uint32_t lo = pack2<T>(c[4 * qd + 0] * mul, c[4 * qd + 1] * mul);
+    const uint32_t hi = pack2<T>(c[4 * qd + 2] * mul, c[4 * qd + 3] * mul);
+    *reinterpret_cast<uint2*>(row_ptr + d0 + 8 * qd + 4 * g) = make_uint2(lo, hi);
+  }
+}
+
+// 2^x on the hardware unit (v_exp_f32); results below 2^-126 may flush to 0,
+// which softmax weights tolerate.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Row index (within a 32-row MFMA tile) held in accumulator element i.
+__device__ __forceinline__ int acc_row(int i, int g) { return 8 * (i >> 2) + 4 * g + (i & 3); }
+
+struct Strides {
+  int64_t row, head;
+};
+
+// ---------------------------------------------------------------- forward
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
+    float* __restrict__ lse, const int32_t* __restrict__ cu, const int32_t* __restrict__ header,
+    const int4* __restrict__ items, int heads, Strides sq, Strides sk, Strides sv, Strides so,
+    float scale, float scale_log2) {
+  constexpr int KLD = D + 8;    // sK leading dim (16-byte pad)
+  constexpr int VLD = kBN + 4;  // sVt leading dim (8-byte pad)
+  __shared__ __align__(16) T sK[kBN * KLD];
+  __shared__ __align__(16) T sVt[D * VLD];
+
+  const int item = blockIdx.x / heads, h = blockIdx.x % heads;
+  if (item >= header[0]) return;
+  const int4 it = items[item];
+  const int start = it.z;
+  const int L = it.w;
+  const int q0 = it.y * kBM;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int g = lane >> 5, lr = lane & 31;
+  const int qw0 = q0 + 32 * wave;
+  const int my_q = qw0 + lr;
+  const bool wave_live = qw0 < L;
+
+  const T* kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
+  const T* vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
+
+  typedef typename VecT<T>::x8 x8;
+  x8 qf[D / 16];
+  {
+    const T* qrow = q + (int64_t)(start + my_q) * sq.row + (int64_t)h * sq.head;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      if (my_q < L) qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
+      else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qf[s][j] = (T)0.f;
+      }
+    }
+  }
+
+  const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
+  const int nkb = (kend_wg + kBN - 1) / kBN;
+  const int kend_wave = wave_live ? (CAUSAL ? min(L, qw0 + 32) : L) : 0;
+
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = zero16();
+  float m_run = kNegInf, l_run = 0.f;
+
+  Stage<T, D, kBN> stK, stV;
+  stK.load(kh, sk.row, 0, L);
+  stV.load(vh, sv.row, 0, L);
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+    stK.put_rows(sK, KLD);
+    stV.put_cols(sVt, VLD);
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      stK.load(kh, sk.row, (kb + 1) * kBN, L);
+      stV.load(vh, sv.row, (kb + 1) * kBN, L);
+    }
+    const int kbase = kb * kBN;
+    const int nt = kbase < kend_wave ? (kbase + 32 < kend_wave ? 2 : 1) : 0;
+    if (nt == 0) continue;
+
+    f32x16 sacc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t < nt) {
+        sacc[t] = zero16();
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s)
+          sacc[t] = mfma32(lds_frag16(sK + (32 * t + lr) * KLD + 16 * s + 8 * g), qf[s], sacc[t]);
+      }
+    }
+    const bool need_mask = (kbase + 32 * nt > L) || (CAUSAL && kbase + 32 * nt - 1 > qw0);
+    if (need_mask) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (t < nt) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = kbase + 32 * t + acc_row(i, g);
+            const bool ok = kk < L && (!CAUSAL || kk <= my_q);
+            if (!ok) sacc[t][i] = kNegInf;
+          }
+        }
+      }
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      if (t < nt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[t][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = fast_exp2((m_run - m_use) * scale_log2);
+    const float mb = m_use * scale_log2;
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      if (t < nt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = fast_exp2(sacc[t][i] * scale_log2 - mb);
+          sacc[t][i] = p;
+          psum += p;
+        }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t < nt) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const x8 pf = pack_frag<T>(sacc[t], 8 * hh);
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt)
+            oacc[dt] = mfma32(lds_frag_2x4(sVt + (32 * dt + lr) * VLD + 32 * t + 16 * hh + 4 * g), pf,
+                              oacc[dt]);
+        }
+      }
+    }
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  if (wave_live && my_q < L) {
+    const float inv_l = 1.0f / l_tot;
+    T* orow = o + (int64_t)(start + my_q) * so.row + (int64_t)h * so.head;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) store_row_slice<T>(orow, 32 * dt, g, oacc[dt], inv_l);
+    if (g == 0) lse[(int64_t)(start + my_q) * heads + h] = m_run * scale + logf(l_tot);
+  }
+}
+
+// -------------------------------------------------- backward: dQ and Delta
+// Per item: 128 queries (32 per wave) loop over 64-key blocks.
+//   S^T = K Q^T, dP^T = V dO^T (Q, dO operands in registers; K, V from LDS)
+//   P^T = exp(S^T - LSE), dS^T = P^T (dP^T - Delta)
+//   dQ^T += K^T dS^T (K^T from LDS, dS^T from registers)
+// Delta = rowsum(O * dO) is computed here from the stored O and written out
+// for the dK/dV pass.
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
+    const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
+    const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
+    float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ header, const int4* __restrict__ items, int heads, Strides sdo,
+    Strides sq, Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2) {
+  constexpr int KLD = D + 8;
+  constexpr int KTLD = kBN + 4;
+  __shared__ __align__(16) T sK[kBN * KLD];
+  __shared__ __align__(16) T sKt[D * KTLD];
+  __shared__ __align__(16) T sV[kBN * KLD];
+
+  const int item = blockIdx.x / heads, h = blockIdx.x % heads;
+  if (item >= header[0]) return;
+  const int4 it = items[item];
+  const int start = it.z;
+  const int L = it.w;
+  const int q0 = it.y * kBM;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int g = lane >> 5, lr = lane & 31;
+  const int qw0 = q0 + 32 * wave;
+  const int my_q = qw0 + lr;
+  const bool wave_live = qw0 < L;
+  const bool row_ok = my_q < L;
+
+  typedef typename VecT<T>::x8 x8;
+  x8 qf[D / 16], df[D / 16];
+  float dl = 0.f;
+  {
+    const int64_t tok = start + my_q;
+    const T* qrow = q + tok * sq.row + (int64_t)h * sq.head;
+    const T* drow = dout + tok * sdo.row + (int64_t)h * sdo.head;
+    const T* orow = o + tok * so.row + (int64_t)h * so.head;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      if (row_ok) {
+        qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
+        df[s] = gmem_frag16(drow + 16 * s + 8 * g);
+        const x8 of = gmem_frag16(orow + 16 * s + 8 * g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)df[s][j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          qf[s][j] = (T)0.f;
+          df[s][j] = (T)0.f;
+        }
+      }
+    }
+  }
+  dl += __shfl_xor(dl, 32, kWave);
+  const float lse2 = row_ok ? lse[(int64_t)(start + my_q) * heads + h] * kLog2e : 0.f;
+  if (row_ok && g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
+
+  const T* kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
+  const T* vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
+  const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
+  const int nkb = (kend_wg + kBN - 1) / kBN;
+  const int kend_wave = wave_live ? (CAUSAL ? min(L, qw0 + 32) : L) : 0;
+
+  f32x16 dqacc[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) dqacc[dt] = zero16();
+
+  Stage<T, D, kBN> stK, stV;
+  stK.load(kh, sk.row, 0, L);
+  stV.load(vh, sv.row, 0, L);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+    stK.put_rows(sK, KLD);
+    stK.put_cols(sKt, KTLD);
+    stV.put_rows(sV, KLD);
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      stK.load(kh, sk.row, (kb + 1) * kBN, L);
+      stV.load(vh, sv.row, (kb + 1) * kBN, L);
+    }
+    const int kbase = kb * kBN;
+    const int nt = kbase < kend_wave ? (kbase + 32 < kend_wave ? 2 : 1) : 0;
+    if (nt == 0) continue;
+    const bool need_mask = (kbase + 32 * nt > L) || (CAUSAL && kbase + 32 * nt - 1 > qw0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t >= nt) continue;
+      f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) {
+        sacc = mfma32(lds_frag16(sK + (32 * t + lr) * KLD + 16 * s + 8 * g), qf[s], sacc);
+        pacc = mfma32(lds_frag16(sV + (32 * t + lr) * KLD + 16 * s + 8 * g), df[s], pacc);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float p = fast_exp2(sacc[i] * scale_log2 - lse2);
+        if (need_mask) {
+          const int kk = kbase + 32 * t + acc_row(i, g);
+          const bool ok = kk < L && (!CAUSAL || kk <= my_q);
+          if (!ok) p = 0.f;
+        }
+        sacc[i] = p * (pacc[i] - dl);  // dS^T
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const x8 sf = pack_frag<T>(sacc, 8 * hh);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+          dqacc[dt] = mfma32(lds_frag_2x4(sKt + (32 * dt + lr) * KTLD + 32 * t + 16 * hh + 4 * g), sf,
+                             dqacc[dt]);
+      }
+    }
+  }
+  if (wave_live && row_ok) {
+    T* out = dq + (int64_t)(start + my_q) * sdq.row + (int64_t)h * sdq.head;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) store_row_slice<T>(out, 32 * dt, g, dqacc[dt], scale);
+  }
+}
+
+// ---------------------------------------------------- backward: dK and dV
+// Per item: 128 keys (32 per wave) loop over blocks of BQ queries.
+//   S = Q K^T, dP = dO V^T (K, V operands in registers; Q, dO from LDS)
+//   P = exp(S - LSE), dS = P (dP - Delta)
+//   dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T from LDS; P, dS in registers)
+// D = 128 holds K, V, dK and dV for 32 keys per lane group in registers and
+// needs the full register file (one wave per SIMD); smaller D fits two.
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kernel(
+    const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
+    const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
+    T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ header, const int4* __restrict__ items, int heads, Strides sdo,
+    Strides sq, Strides sk, Strides sv, Strides sdk, Strides sdv, float scale, float scale_log2) {
+  constexpr int BQ = D >= 128 ? 32 : 64;
+  constexpr int NQT = BQ / 32;
+  constexpr int LD = D + 8;
+  constexpr int TLD = BQ + 4;
+  __shared__ __align__(16) T sQ[BQ * LD];
+  __shared__ __align__(16) T sQt[D * TLD];
+  __shared__ __align__(16) T sO[BQ * LD];   // dO rows
+  __shared__ __align__(16) T sOt[D * TLD];  // dO transposed
+  __shared__ __align__(16) float sL[BQ];
+  __shared__ __align__(16) float sDl[BQ];
+
+  const int item = blockIdx.x / heads, h = blockIdx.x % heads;
+  if (item >= header[0]) return;
+  const int4 it = items[item];
+  const int start = it.z;
+  const int L = it.w;
+  const int nblk = (L + kBM - 1) / kBM;
+  const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int g = lane >> 5, lr = lane & 31;
+  const int kw0 = k0 + 32 * wave;
+  const int my_k = kw0 + lr;
+  const bool wave_live = kw0 < L;
+  const bool key_ok = my_k < L;
+
+  typedef typename VecT<T>::x8 x8;
+  x8 kf[D / 16], vf[D / 16];
+  {
+    const T* krow = k + (int64_t)(start + my_k) * sk.row + (int64_t)h * sk.head;
+    const T* vrow = v + (int64_t)(start + my_k) * sv.row + (int64_t)h * sv.head;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      if (key_ok) {
+        kf[s] = gmem_frag16(krow + 16 * s + 8 * g);
+        vf[s] = gmem_frag16(vrow + 16 * s + 8 * g);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          kf[s][j] = (T)0.f;
+          vf[s][j] = (T)0.f;
+        }
+      }
+    }
+  }
+  f32x16 dkacc[D / 32], dvacc[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) {
+    dkacc[dt] = zero16();
+    dvacc[dt] = zero16();
+  }
+
+  const T* qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
+  const T* dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
+  const int qbeg = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
+  const int nqb = L > qbeg ? (L - qbeg + BQ - 1) / BQ : 0;
+
+  Stage<T, D, BQ> stQ, stO;
+  float pl = 0.f, pd = 0.f;
+  auto load_block = [&](int qb) {
+    stQ.load(qh, sq.row, qb, L);
+    stO.load(dh, sdo.row, qb, L);
+    if (threadIdx.x < BQ) {
+      const int qq = qb + threadIdx.x;
+      pl = qq < L ? lse[(int64_t)(start + qq) * heads + h] * kLog2e : 0.f;
+      pd = qq < L ? delta[(int64_t)(start + qq) * heads + h] : 0.f;
+    }
+  };
+  if (nqb > 0) load_block(qbeg);
+  for (int b = 0; b < nqb; ++b) {
+    const int qb = qbeg + b * BQ;
+    __syncthreads();
+    stQ.put_rows(sQ, LD);
+    stQ.put_cols(sQt, TLD);
+    stO.put_rows(sO, LD);
+    stO.put_cols(sOt, TLD);
+    if (threadIdx.x < BQ) {
+      sL[threadIdx.x] = pl;
+      sDl[threadIdx.x] = pd;
+    }
+    __syncthreads();
+    if (b + 1 < nqb) load_block(qb + BQ);
+    if (!wave_live) continue;
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+      const int qt0 = qb + 32 * u;
+      if (qt0 >= L) continue;
+      if (CAUSAL && qt0 + 31 < kw0) continue;  // every query of the tile precedes every key
+      f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) {
+        sacc = mfma32(lds_frag16(sQ + (32 * u + lr) * LD + 16 * s + 8 * g), kf[s], sacc);
+        pacc = mfma32(lds_frag16(sO + (32 * u + lr) * LD + 16 * s + 8 * g), vf[s], pacc);
+      }
+      // lane: key my_k (column), queries qt0 + acc_row(i, g) (rows)
+      const bool need_mask = (qt0 + 32 > L) || (CAUSAL && qt0 < kw0 + 31);
+      float pv[16];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int r0 = 32 * u + 8 * i4 + 4 * g;
+        const float4 l4 = *reinterpret_cast<const float4*>(sL + r0);
+        const float4 d4 = *reinterpret_cast<const float4*>(sDl + r0);
+        const float la[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float da[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * i4 + e;
+          float p = fast_exp2(sacc[i] * scale_log2 - la[e]);
+          if (need_mask) {
+            const int qq = qt0 + acc_row(i, g);
+            const bool ok = qq < L && (!CAUSAL || qq >= my_k);
+            if (!ok) p = 0.f;
+          }
+          pv[i] = p;
+          sacc[i] = p * (pacc[i] - da[e]);  // dS
+        }
+      }
+      f32x16 pacc2;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pacc2[i] = pv[i];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const x8 pf = pack_frag<T>(pacc2, 8 * hh);
+        const x8 sf = pack_frag<T>(sacc, 8 * hh);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          dvacc[dt] = mfma32(lds_frag_2x4(sOt + (32 * dt + lr) * TLD + 32 * u + 16 * hh + 4 * g), pf,
+                             dvacc[dt]);
+          dkacc[dt] = mfma32(lds_frag_2x4(sQt + (32 * dt + lr) * TLD + 32 * u + 16 * hh + 4 * g), sf,
+                             dkacc[dt]);
+        }
+      }
+    }
+  }
+  if (wave_live && key_ok) {
+    T* krow = dk + (int64_t)(start + my_k) * sdk.row + (int64_t)h * sdk.head;
+    T* vrow = dv + (int64_t)(start + my_k) * sdv.row + (int64_t)h * sdv.head;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      store_row_slice<T>(krow, 32 * dt, g, dkacc[dt], scale);
+      store_row_slice<T>(vrow, 32 * dt, g, dvacc[dt], 1.0f);
+    }
+  }
+}
+
+// ------------------------------------------------------------------- host
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_tensor(const char* fn, const char* name, const void* p, const int64_t* st, int heads,
+                 int head_dim, int64_t total) {
+  if (!p) return set_error(SCREE_ERR_INVALID, "%s: %s is null", fn, name);
+  if (!aligned16(p)) return set_error(SCREE_ERR_INVALID, "%s: %s is not 16-byte aligned", fn, name);
+  if (st[0] % 8 || st[1] % 8 || st[0] < 0 || st[1] < 0)
+    return set_error(SCREE_ERR_INVALID,
+                     "%s: %s strides (%lld, %lld) must be non-negative multiples of 8 elements",
+                     fn, name, (long long)st[0], (long long)st[1]);
+  if (total > 1 && st[0] < head_dim)
+    return set_error(SCREE_ERR_INVALID, "%s: %s row stride %lld overlaps rows", fn, name,
+                     (long long)st[0]);
+  (void)heads;
+  return SCREE_OK;
+}
+
+int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, int heads,
+                 int head_dim, int dtype, const void* workspace, size_t workspace_bytes) {
+  if (!cu) return set_error(SCREE_ERR_INVALID, "%s: cu_seqlens is null", fn);
+  if (batch < 1 || batch > kMaxBatch)
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: batch must be in [1, %d], got %d", fn, kMaxBatch,
+                     batch);
+  if (total < 0 || total > ((int64_t)1 << 30))
+    return set_error(SCREE_ERR_INVALID, "%s: total_tokens %lld out of range", fn, (long long)total);
+  if (heads < 1 || heads > 4096)
+    return set_error(SCREE_ERR_INVALID, "%s: heads must be in [1, 4096], got %d", fn, heads);
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (32, 64, 128)", fn,
+                     head_dim);
+  if (dtype != SCREE_DTYPE_F16 && dtype != SCREE_DTYPE_BF16)
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: dtype code %d unsupported (fp16 / bf16 only)", fn,
+                     dtype);
+  const size_t need = scree_attn_workspace_bytes(batch, total, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return set_error(SCREE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
+                     workspace ? workspace_bytes : (size_t)0);
+  if (tmax_for(batch, total) * heads > 0x7fffffffLL)
+    return set_error(SCREE_ERR_INVALID, "%s: grid too large", fn);
+  return SCREE_OK;
+}
+
+template <typename T, int D, bool C>
+void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
+                  const int32_t* cu, int heads, const int64_t* st, float scale, int64_t grid,
+                  const void* ws, hipStream_t stream) {
+  const int32_t* header = static_cast<const int32_t*>(ws);
+  const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
+  hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                     static_cast<T*>(o), lse, cu, header, items, heads, Strides{st[0], st[1]},
+                     Strides{st[2], st[3]}, Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale,
+                     scale * kLog2e);
+}
+
+template <typename T, int D, bool C>
+void launch_bwd_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
+                  const float* lse, void* dq, void* dk, void* dv, float* delta, const int32_t* cu,
+                  int heads, const int64_t* st, float scale, int64_t grid, const void* ws,
+                  hipStream_t stream) {
+  const int32_t* header = static_cast<const int32_t*>(ws);
+  const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
+  const Strides sdo{st[0], st[1]}, sq{st[2], st[3]}, sk{st[4], st[5]}, sv{st[6], st[7]},
+      so{st[8], st[9]}, sdq{st[10], st[11]}, sdk{st[12], st[13]}, sdv{st[14], st[15]};
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                     static_cast<const T*>(dout), static_cast<const T*>(q),
+                     static_cast<const T*>(k), static_cast<const T*>(v),
+                     static_cast<const T*>(o), lse, delta, static_cast<T*>(dq), cu, header, items,
+                     heads, sdo, sq, sk, sv, so, sdq, scale, scale * kLog2e);
+  hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0,
+                     stream, static_cast<const T*>(dout), static_cast<const T*>(q),
+                     static_cast<const T*>(k), static_cast<const T*>(v), lse,
+                     static_cast<const float*>(delta), static_cast<T*>(dk), static_cast<T*>(dv),
+                     cu, header, items, heads, sdo, sq, sk, sv, sdk, sdv, scale, scale * kLog2e);
+}
+
+#define SCREE_DISPATCH(FN, dtype, D, causal, ...)                                 \
+  do {                                                                            \
+    if (dtype == SCREE_DTYPE_F16) {                                               \
+      if (D == 32) { if (causal) FN<f16, 32, true>(__VA_ARGS__); else FN<f16, 32, false>(__VA_ARGS__); } \
+      else if (D == 64) { if (causal) FN<f16, 64, true>(__VA_ARGS__); else FN<f16, 64, false>(__VA_ARGS__); } \
+      else { if (causal) FN<f16, 128, true>(__VA_ARGS__); else FN<f16, 128, false>(__VA_ARGS__); } \
+    } else {                                                                      \
+      if (D == 32) { if (causal) FN<bf16, 32, true>(__VA_ARGS__); else FN<bf16, 32, false>(__VA_ARGS__); } \
+      else if (D == 64) { if (causal) FN<bf16, 64, true>(__VA_ARGS__); else FN<bf16, 64, false>(__VA_ARGS__); } \
+      else { if (causal) FN<bf16, 128, true>(__VA_ARGS__); else FN<bf16, 128, false>(__VA_ARGS__); } \
+    }                                                                             \
+  } while (0)
+
+}  // namespace
+}  // namespace scree
+
+using namespace scree;
+
+extern "C" size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim) {
+  (void)head_dim;
+  if (batch < 1 || total_tokens < 0) return 0;
+  return kHeaderBytes + (size_t)tmax_for(batch, total_tokens) * sizeof(int4);
+}
+
+extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                                   int head_dim, int causal, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  const char* fn = "scree_attn_schedule";
+  if (!cu_seqlens) return set_error(SCREE_ERR_INVALID, "%s: cu_seqlens is null", fn);
+  if (batch < 1 || batch > kMaxBatch)
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: batch must be in [1, %d], got %d", fn, kMaxBatch,
+                     batch);
+  if (total_tokens < 0 || total_tokens > ((int64_t)1 << 30))
+    return set_error(SCREE_ERR_INVALID, "%s: total_tokens %lld out of range", fn,
+                     (long long)total_tokens);
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (32, 64, 128)", fn,
+                     head_dim);
+  const size_t need = scree_attn_workspace_bytes(batch, total_tokens, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return set_error(SCREE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
+                     workspace ? workspace_bytes : (size_t)0);
+  int32_t* header = static_cast<int32_t*>(workspace);
+  int4* items = reinterpret_cast<int4*>(static_cast<char*>(workspace) + kHeaderBytes);
+  hipLaunchKernelGGL(attn_schedule_kernel, dim3(1), dim3(1024), 0,
+                     static_cast<hipStream_t>(stream), cu_seqlens, batch, (int)total_tokens,
+                     causal ? 1 : 0, (int)tmax_for(batch, total_tokens), header, items);
+  return check_launch(fn);
+}
+
+extern "C" int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                              const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                              int heads, int head_dim, const int64_t* strides, float softmax_scale,
+                              int causal, int dtype, const void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const char* fn = "scree_attn_fwd";
+  int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
+                        workspace_bytes);
+  if (rc) return rc;
+  if (!strides) return set_error(SCREE_ERR_INVALID, "%s: strides is null", fn);
+  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  const char* names[4] = {"q", "k", "v", "o"};
+  const void* ptrs[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    rc = check_tensor(fn, names[i], ptrs[i], strides + 2 * i, heads, head_dim, total_tokens);
+    if (rc) return rc;
+  }
+  if (total_tokens == 0) return SCREE_OK;
+  const int64_t grid = tmax_for(batch, total_tokens) * heads;
+  SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, heads,
+                 strides, softmax_scale, grid, workspace, static_cast<hipStream_t>(stream));
+  return check_launch(fn);
+}
+
+extern "C" int scree_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
+                              const void* o, const float* lse, void* dq, void* dk, void* dv,
+                              float* delta, const int32_t* cu_seqlens, int batch,
+                              int64_t total_tokens, int heads, int head_dim,
+                              const int64_t* strides, float softmax_scale, int causal, int dtype,
+                              const void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "scree_attn_bwd";
+  int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
+                        workspace_bytes);
+  if (rc) return rc;
+  if (!strides) return set_error(SCREE_ERR_INVALID, "%s: strides is null", fn);
+  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  if (!delta || !aligned16(delta))
+    return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
+  const char* names[8] = {"dout", "q", "k", "v", "o", "dq", "dk", "dv"};
+  const void* ptrs[8] = {dout, q, k, v, o, dq, dk, dv};
+  for (int i = 0; i < 8; ++i) {
+    rc = check_tensor(fn, names[i], ptrs[i], strides + 2 * i, heads, head_dim, total_tokens);
+    if (rc) return rc;
+  }
+  if (total_tokens == 0) return SCREE_OK;
+  const int64_t grid = tmax_for(batch, total_tokens) * heads;
+  SCREE_DISPATCH(launch_bwd_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, dk, dv, delta,
+                 cu_seqlens, heads, strides, softmax_scale, grid, workspace,
+                 static_cast<hipStream_t>(stream));
+  return check_launch(fn);
+}

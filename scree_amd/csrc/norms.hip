@@ -1,0 +1,579 @@
+// Varlen RMSNorm / LayerNorm, forward and backward, for gfx950.
+//
+// Norms act per token row, so the packed (rows, dim) buffer is processed
+// with no reference to the offsets (the reference's kernels ignore them too,
+// src/scree/kernels/triton/varlen_rmsnorm.py:7-8).
+//
+// Fast path: one wavefront per row.  Each lane keeps CHUNKS 16-byte vectors
+// of the row in registers (dim = CHUNKS * 64 lanes * 16 bytes at most), so x
+// is read from HBM exactly once; the reductions are wave-wide shuffles.
+// Generic path (dim not a multiple of one 16-byte vector, unaligned buffers,
+// or rows longer than the fast path holds): one wavefront per row looping
+// over the columns.
+//
+// Backward writes dx per row and accumulates the parameter gradients in fp32
+// registers of each wave over the rows it owns; the waves of a block then sum
+// their partials in LDS in a fixed order and write one partial row per block;
+// a column-sum kernel adds the partial rows in a fixed order.  No atomics:
+// results are bit-identical from run to run.
+#include <initializer_list>
+
+#include "common.h"
+
+namespace scree {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kFwdWaves = 4;       // rows (waves) per forward block
+constexpr int kBwdWaves = 8;       // waves per backward block
+constexpr int kMaxParts = 512;     // partial rows of a backward, at most
+constexpr int kMaxChunks = 16;     // 16-byte vectors per lane on the fast path
+
+// ------------------------------------------------------------------ forward
+template <typename T, int CHUNKS, bool LAYER>
+__global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ b, T* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows, int dim, float eps) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x / kWave);
+  if (row >= rows) return;
+  const int nvec = dim / VEC;
+  const T* xr = x + row * (int64_t)dim;
+  uint4 v[CHUNKS];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int vi = c * kWave + lane;
+    v[c] = vi < nvec ? ld16(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+  }
+  const float fdim = (float)dim;
+  float mu = 0.f, rstd;
+  if (LAYER) {
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += elem<T>(v[c], e);
+    mu = wave_sum(s) / fdim;
+    float s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      if (c * kWave + lane < nvec) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float d = elem<T>(v[c], e) - mu;
+          s2 += d * d;
+        }
+      }
+    }
+    rstd = 1.0f / sqrtf(wave_sum(s2) / fdim + eps);
+  } else {
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float t = elem<T>(v[c], e);
+        s += t * t;
+      }
+    rstd = 1.0f / sqrtf(wave_sum(s) / fdim + eps);
+  }
+  T* yr = y + row * (int64_t)dim;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int vi = c * kWave + lane;
+    if (vi < nvec) {
+      uint4 wv = make_uint4(0, 0, 0, 0), bv = make_uint4(0, 0, 0, 0);
+      if (w) wv = ld16(w + (int64_t)vi * VEC);
+      if (LAYER && b) bv = ld16(b + (int64_t)vi * VEC);
+      float f[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float t = LAYER ? (elem<T>(v[c], e) - mu) * rstd : elem<T>(v[c], e) * rstd;
+        if (w) t *= elem<T>(wv, e);
+        if (LAYER && b) t += elem<T>(bv, e);
+        f[e] = t;
+      }
+      st16(yr + (int64_t)vi * VEC, pack16<T>(f));
+    }
+  }
+  if (lane == 0) {
+    if (rstd_out) rstd_out[row] = rstd;
+    if (LAYER && mean_out) mean_out[row] = mu;
+  }
+}
+
+template <typename T, bool LAYER>
+__global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_generic(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ b, T* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows, int dim, float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x / kWave);
+  if (row >= rows) return;
+  const T* xr = x + row * (int64_t)dim;
+  const float fdim = (float)dim;
+  float mu = 0.f, rstd;
+  if (LAYER) {
+    float s = 0.f;
+    for (int j = lane; j < dim; j += kWave) s += to_f32(xr[j]);
+    mu = wave_sum(s) / fdim;
+    float s2 = 0.f;
+    for (int j = lane; j < dim; j += kWave) {
+      const float d = to_f32(xr[j]) - mu;
+      s2 += d * d;
+    }
+    rstd = 1.0f / sqrtf(wave_sum(s2) / fdim + eps);
+  } else {
+    float s = 0.f;
+    for (int j = lane; j < dim; j += kWave) {
+      const float t = to_f32(xr[j]);
+      s += t * t;
+    }
+    rstd = 1.0f / sqrtf(wave_sum(s) / fdim + eps);
+  }
+  T* yr = y + row * (int64_t)dim;
+  for (int j = lane; j < dim; j += kWave) {
+    float t = LAYER ? (to_f32(xr[j]) - mu) * rstd : to_f32(xr[j]) * rstd;
+    if (w) t *= to_f32(w[j]);
+    if (LAYER && b) t += to_f32(b[j]);
+    yr[j] = from_f32<T>(t);
+  }
+  if (lane == 0) {
+    if (rstd_out) rstd_out[row] = rstd;
+    if (LAYER && mean_out) mean_out[row] = mu;
+  }
+}
+
+// ----------------------------------------------------------------- backward
+// partial layout: [part][param][dim] fp32, param 0 = dweight, 1 = dbias.
+template <typename T, int CHUNKS, bool LAYER>
+__global__ __launch_bounds__(kBwdWaves* kWave) void norm_bwd_vec(
+    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
+    const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ dx,
+    float* __restrict__ partial, int64_t rows, int dim, int nparam) {
+  constexpr int VEC = 16 / sizeof(T);
+  extern __shared__ float red[];  // dim floats
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nvec = dim / VEC;
+  const float fdim = (float)dim;
+  float aw[CHUNKS][VEC];
+  float ab[LAYER ? CHUNKS : 1][VEC];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      aw[c][e] = 0.f;
+      if (LAYER) ab[LAYER ? c : 0][e] = 0.f;
+    }
+
+  for (int64_t row = (int64_t)blockIdx.x * kBwdWaves + wave; row < rows;
+       row += (int64_t)gridDim.x * kBwdWaves) {
+    const T* xr = x + row * (int64_t)dim;
+    const T* gr = dy + row * (int64_t)dim;
+    uint4 xv[CHUNKS], gv[CHUNKS];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int vi = c * kWave + lane;
+      xv[c] = vi < nvec ? ld16(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+      gv[c] = vi < nvec ? ld16(gr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+    }
+    const float r = rstd_in[row];
+    const float mu = LAYER ? mean_in[row] : 0.f;
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int vi = c * kWave + lane;
+      if (vi < nvec) {
+        uint4 wv = make_uint4(0, 0, 0, 0);
+        if (w) wv = ld16(w + (int64_t)vi * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float xx = elem<T>(xv[c], e);
+          const float d = elem<T>(gv[c], e);
+          const float g = w ? d * elem<T>(wv, e) : d;
+          if (LAYER) {
+            const float xh = (xx - mu) * r;
+            s1 += g;
+            s2 += g * xh;
+            aw[c][e] += d * xh;
+            ab[LAYER ? c : 0][e] += d;
+          } else {
+            s1 += xx * g;
+            aw[c][e] += d * xx * r;
+          }
+        }
+      }
+    }
+    s1 = wave_sum(s1);
+    if (LAYER) s2 = wave_sum(s2);
+    const float k_rms = r * r * r * s1 / fdim;
+    const float a_ln = s1 / fdim;
+    const float b_ln = s2 / fdim;
+    T* dxr = dx + row * (int64_t)dim;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int vi = c * kWave + lane;
+      if (vi < nvec) {
+        uint4 wv = make_uint4(0, 0, 0, 0);
+        if (w) wv = ld16(w + (int64_t)vi * VEC);
+        float f[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float xx = elem<T>(xv[c], e);
+          const float d = elem<T>(gv[c], e);
+          const float g = w ? d * elem<T>(wv, e) : d;
+          if (LAYER) {
+            const float xh = (xx - mu) * r;
+            f[e] = r * (g - a_ln - xh * b_ln);
+          } else {
+            f[e] = r * g - k_rms * xx;
+          }
+        }
+        st16(dxr + (int64_t)vi * VEC, pack16<T>(f));
+      }
+    }
+  }
+
+  // Fixed-order block reduction of the per-wave parameter partials.
+  for (int p = 0; p < nparam; ++p) {
+    for (int turn = 0; turn < kBwdWaves; ++turn) {
+      if (wave == turn) {
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+          const int vi = c * kWave + lane;
+          if (vi < nvec) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+              const float a = (p == 0) ? aw[c][e] : ab[LAYER ? c : 0][e];
+              const int idx = vi * VEC + e;
+              red[idx] = turn == 0 ? a : red[idx] + a;
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+    float* out = partial + ((int64_t)blockIdx.x * nparam + p) * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = red[i];
+    __syncthreads();
+  }
+}
+
+template <typename T, bool LAYER>
+__global__ __launch_bounds__(kFwdWaves* kWave) void norm_bwd_dx_generic(
+    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
+    const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ dx,
+    int64_t rows, int dim) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x / kWave);
+  if (row >= rows) return;
+  const T* xr = x + row * (int64_t)dim;
+  const T* gr = dy + row * (int64_t)dim;
+  const float r = rstd_in[row];
+  const float mu = LAYER ? mean_in[row] : 0.f;
+  const float fdim = (float)dim;
+  float s1 = 0.f, s2 = 0.f;
+  for (int j = lane; j < dim; j += kWave) {
+    const float xx = to_f32(xr[j]);
+    const float d = to_f32(gr[j]);
+    const float g = w ? d * to_f32(w[j]) : d;
+    if (LAYER) {
+      s1 += g;
+      s2 += g * ((xx - mu) * r);
+    } else {
+      s1 += xx * g;
+    }
+  }
+  s1 = wave_sum(s1);
+  if (LAYER) s2 = wave_sum(s2);
+  const float k_rms = r * r * r * s1 / fdim;
+  const float a_ln = s1 / fdim;
+  const float b_ln = s2 / fdim;
+  T* dxr = dx + row * (int64_t)dim;
+  for (int j = lane; j < dim; j += kWave) {
+    const float xx = to_f32(xr[j]);
+    const float d = to_f32(gr[j]);
+    const float g = w ? d * to_f32(w[j]) : d;
+    const float v = LAYER ? r * (g - a_ln - ((xx - mu) * r) * b_ln) : r * g - k_rms * xx;
+    dxr[j] = from_f32<T>(v);
+  }
+}
+
+// grid (ceil(dim/256), nparts): thread owns one column, sums rows part, part+nparts, ...
+template <typename T, bool LAYER>
+__global__ __launch_bounds__(256) void norm_bwd_param_generic(
+    const T* __restrict__ dy, const T* __restrict__ x, const float* __restrict__ mean_in,
+    const float* __restrict__ rstd_in, float* __restrict__ partial, int64_t rows, int dim,
+    int nparam) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  const int part = blockIdx.y;
+  const int nparts = gridDim.y;
+  if (col >= dim) return;
+  float aw = 0.f, ab = 0.f;
+  for (int64_t row = part; row < rows; row += nparts) {
+    const float xx = to_f32(x[row * (int64_t)dim + col]);
+    const float d = to_f32(dy[row * (int64_t)dim + col]);
+    const float r = rstd_in[row];
+    if (LAYER) {
+      aw += d * ((xx - mean_in[row]) * r);
+      ab += d;
+    } else {
+      aw += d * xx * r;
+    }
+  }
+  float* out = partial + (int64_t)part * nparam * dim;
+  out[col] = aw;
+  if (nparam > 1) out[dim + col] = ab;
+}
+
+// Column sums of the partial rows, in part order; output cast to out_dtype.
+__global__ __launch_bounds__(256) void norm_param_colsum(const float* __restrict__ partial,
+                                                         int nparts, int nparam, int dim,
+                                                         void* out0, void* out1, int out_dtype) {
+  __shared__ float red[4][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int grp = threadIdx.x / kWave;
+  const int col = blockIdx.x * kWave + lane;
+  const int p = blockIdx.y;
+  float s = 0.f;
+  if (col < dim) {
+    for (int i = grp; i < nparts; i += 4) s += partial[((int64_t)i * nparam + p) * dim + col];
+  }
+  red[grp][lane] = s;
+  __syncthreads();
+  if (grp == 0 && col < dim) {
+    const float t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    void* out = p == 0 ? out0 : out1;
+    if (out) {
+      if (out_dtype == SCREE_DTYPE_F32) static_cast<float*>(out)[col] = t;
+      else if (out_dtype == SCREE_DTYPE_F16) static_cast<f16*>(out)[col] = (f16)t;
+      else static_cast<bf16*>(out)[col] = (bf16)t;
+    }
+  }
+}
+
+// --------------------------------------------------------------------- host
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int chunks_for(int nvec) {
+  int need = (nvec + kWave - 1) / kWave;
+  int c = 1;
+  while (c < need) c <<= 1;
+  return c;
+}
+
+inline int nparts_for(int64_t rows) {
+  int64_t p = (rows + kBwdWaves - 1) / kBwdWaves;
+  if (p < 1) p = 1;
+  if (p > kMaxParts) p = kMaxParts;
+  return (int)p;
+}
+
+template <typename T>
+bool fast_path_ok(int64_t dim, std::initializer_list<const void*> ptrs) {
+  constexpr int VEC = 16 / sizeof(T);
+  if (dim % VEC) return false;
+  if (dim / VEC > (int64_t)kMaxChunks * kWave) return false;
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return false;
+  return true;
+}
+
+template <typename T, bool LAYER>
+int launch_fwd(const void* x, const void* w, const void* b, void* y, float* mean, float* rstd,
+               int64_t rows, int64_t dim, float eps, hipStream_t stream) {
+  const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
+  const dim3 block(kFwdWaves * kWave);
+  const T* xp = static_cast<const T*>(x);
+  const T* wp = static_cast<const T*>(w);
+  const T* bp = static_cast<const T*>(b);
+  T* yp = static_cast<T*>(y);
+  const int d = (int)dim;
+  if (fast_path_ok<T>(dim, {x, w, b, y})) {
+    const int chunks = chunks_for((int)(dim / (16 / sizeof(T))));
+#define SCREE_FWD_CASE(C)                                                                        \
+  case C:                                                                                        \
+    hipLaunchKernelGGL((norm_fwd_vec<T, C, LAYER>), grid, block, 0, stream, xp, wp, bp, yp, mean, \
+                       rstd, rows, d, eps);                                                      \
+    break;
+    switch (chunks) {
+      SCREE_FWD_CASE(1)
+      SCREE_FWD_CASE(2)
+      SCREE_FWD_CASE(4)
+      SCREE_FWD_CASE(8)
+      SCREE_FWD_CASE(16)
+      default:
+        return set_error(SCREE_ERR_INVALID, "norm forward: internal chunk count %d", chunks);
+    }
+#undef SCREE_FWD_CASE
+  } else {
+    hipLaunchKernelGGL((norm_fwd_generic<T, LAYER>), grid, block, 0, stream, xp, wp, bp, yp, mean,
+                       rstd, rows, d, eps);
+  }
+  return check_launch(LAYER ? "scree_layernorm_fwd" : "scree_rmsnorm_fwd");
+}
+
+template <typename T, bool LAYER>
+int launch_bwd(const void* dy, const void* x, const void* w, const float* mean, const float* rstd,
+               void* dx, void* dw, void* db, int dparam_dtype, int64_t rows, int64_t dim,
+               void* workspace, hipStream_t stream) {
+  const T* dyp = static_cast<const T*>(dy);
+  const T* xp = static_cast<const T*>(x);
+  const T* wp = static_cast<const T*>(w);
+  T* dxp = static_cast<T*>(dx);
+  const int d = (int)dim;
+  const int nparam = LAYER ? 2 : 1;
+  const bool want_params = (dw != nullptr) || (db != nullptr);
+  const int nparts = nparts_for(rows);
+  float* partial = static_cast<float*>(workspace);
+  if (fast_path_ok<T>(dim, {dy, x, w, dx})) {
+    const int chunks = chunks_for((int)(dim / (16 / sizeof(T))));
+    const dim3 grid((unsigned)nparts), block(kBwdWaves * kWave);
+    const size_t lds = (size_t)d * sizeof(float);
+    const int np = want_params ? nparam : 0;
+#define SCREE_BWD_CASE(C)                                                                        \
+  case C:                                                                                        \
+    hipLaunchKernelGGL((norm_bwd_vec<T, C, LAYER>), grid, block, lds, stream, dyp, xp, wp, mean,  \
+                       rstd, dxp, partial, rows, d, np);                                         \
+    break;
+    switch (chunks) {
+      SCREE_BWD_CASE(1)
+      SCREE_BWD_CASE(2)
+      SCREE_BWD_CASE(4)
+      SCREE_BWD_CASE(8)
+      SCREE_BWD_CASE(16)
+      default:
+        return set_error(SCREE_ERR_INVALID, "norm backward: internal chunk count %d", chunks);
+    }
+#undef SCREE_BWD_CASE
+  } else {
+    const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves)), block(kFwdWaves * kWave);
+    if (rows > 0)
+      hipLaunchKernelGGL((norm_bwd_dx_generic<T, LAYER>), grid, block, 0, stream, dyp, xp, wp,
+                         mean, rstd, dxp, rows, d);
+    if (want_params) {
+      const dim3 pgrid((unsigned)((dim + 255) / 256), (unsigned)nparts);
+      hipLaunchKernelGGL((norm_bwd_param_generic<T, LAYER>), pgrid, dim3(256), 0, stream, dyp, xp,
+                         mean, rstd, partial, rows, d, nparam);
+    }
+  }
+  int rc = check_launch(LAYER ? "scree_layernorm_bwd" : "scree_rmsnorm_bwd");
+  if (rc != SCREE_OK || !want_params) return rc;
+  const dim3 cgrid((unsigned)((dim + kWave - 1) / kWave), (unsigned)nparam);
+  hipLaunchKernelGGL(norm_param_colsum, cgrid, dim3(256), 0, stream, partial, nparts, nparam, d, dw,
+                     db, dparam_dtype);
+  return check_launch(LAYER ? "scree_layernorm_bwd (param sum)" : "scree_rmsnorm_bwd (param sum)");
+}
+
+int validate_common(const char* fn, int64_t rows, int64_t dim, int dtype) {
+  if (rows < 0 || rows >= ((int64_t)1 << 31))
+    return set_error(SCREE_ERR_INVALID, "%s: rows must be in [0, 2^31), got %lld", fn, (long long)rows);
+  if (dim < 1 || dim > (1 << 24))
+    return set_error(SCREE_ERR_INVALID, "%s: dim must be in [1, 2^24], got %lld", fn, (long long)dim);
+  if (dtype != SCREE_DTYPE_F32 && dtype != SCREE_DTYPE_F16 && dtype != SCREE_DTYPE_BF16)
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: unknown dtype code %d", fn, dtype);
+  if (rows * dim >= ((int64_t)1 << 40))
+    return set_error(SCREE_ERR_INVALID, "%s: tensor too large", fn);
+  return SCREE_OK;
+}
+
+}  // namespace
+}  // namespace scree
+
+using namespace scree;
+
+extern "C" size_t scree_norm_bwd_workspace_bytes(int64_t rows, int64_t dim) {
+  if (rows < 0 || dim < 1) return 0;
+  return (size_t)nparts_for(rows) * 2u * (size_t)dim * sizeof(float);
+}
+
+extern "C" int scree_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd,
+                                 int64_t rows, int64_t dim, float eps, int dtype, void* stream) {
+  const char* fn = "scree_rmsnorm_fwd";
+  int rc = validate_common(fn, rows, dim, dtype);
+  if (rc) return rc;
+  if (rows == 0) return SCREE_OK;
+  if (!x || !y) return set_error(SCREE_ERR_INVALID, "%s: x and y must be non-null", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32: return launch_fwd<float, false>(x, weight, nullptr, y, nullptr, rstd, rows, dim, eps, s);
+    case SCREE_DTYPE_F16: return launch_fwd<f16, false>(x, weight, nullptr, y, nullptr, rstd, rows, dim, eps, s);
+    default: return launch_fwd<bf16, false>(x, weight, nullptr, y, nullptr, rstd, rows, dim, eps, s);
+  }
+}
+
+extern "C" int scree_layernorm_fwd(const void* x, const void* weight, const void* bias, void* y,
+                                   float* mean, float* rstd, int64_t rows, int64_t dim, float eps,
+                                   int dtype, void* stream) {
+  const char* fn = "scree_layernorm_fwd";
+  int rc = validate_common(fn, rows, dim, dtype);
+  if (rc) return rc;
+  if (rows == 0) return SCREE_OK;
+  if (!x || !y) return set_error(SCREE_ERR_INVALID, "%s: x and y must be non-null", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32: return launch_fwd<float, true>(x, weight, bias, y, mean, rstd, rows, dim, eps, s);
+    case SCREE_DTYPE_F16: return launch_fwd<f16, true>(x, weight, bias, y, mean, rstd, rows, dim, eps, s);
+    default: return launch_fwd<bf16, true>(x, weight, bias, y, mean, rstd, rows, dim, eps, s);
+  }
+}
+
+static int validate_bwd(const char* fn, const void* dy, const void* x, const float* rstd, void* dx,
+                        bool want_params, int dparam_dtype, int64_t rows, int64_t dim,
+                        void* workspace, size_t workspace_bytes) {
+  if (!dy || !x || !rstd || !dx)
+    return set_error(SCREE_ERR_INVALID, "%s: dy, x, rstd and dx must be non-null", fn);
+  if (want_params) {
+    if (dparam_dtype != SCREE_DTYPE_F32 && dparam_dtype != SCREE_DTYPE_F16 &&
+        dparam_dtype != SCREE_DTYPE_BF16)
+      return set_error(SCREE_ERR_UNSUPPORTED, "%s: unknown parameter dtype code %d", fn, dparam_dtype);
+    const size_t need = scree_norm_bwd_workspace_bytes(rows, dim);
+    if (!workspace || workspace_bytes < need)
+      return set_error(SCREE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
+                       workspace ? workspace_bytes : (size_t)0);
+  }
+  return SCREE_OK;
+}
+
+extern "C" int scree_rmsnorm_bwd(const void* dy, const void* x, const void* weight,
+                                 const float* rstd, void* dx, void* dweight, int dparam_dtype,
+                                 int64_t rows, int64_t dim, int dtype, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  const char* fn = "scree_rmsnorm_bwd";
+  int rc = validate_common(fn, rows, dim, dtype);
+  if (rc) return rc;
+  if (dweight && !weight) return set_error(SCREE_ERR_INVALID, "%s: dweight requires weight", fn);
+  if (rows == 0 && !dweight) return SCREE_OK;  // nothing to write; empty dweight is summed to 0 below
+  rc = validate_bwd(fn, dy, x, rstd, dx, dweight != nullptr, dparam_dtype, rows, dim, workspace,
+                    workspace_bytes);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32: return launch_bwd<float, false>(dy, x, weight, nullptr, rstd, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+    case SCREE_DTYPE_F16: return launch_bwd<f16, false>(dy, x, weight, nullptr, rstd, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+    default: return launch_bwd<bf16, false>(dy, x, weight, nullptr, rstd, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+  }
+}
+
+extern "C" int scree_layernorm_bwd(const void* dy, const void* x, const void* weight,
+                                   const float* mean, const float* rstd, void* dx, void* dweight,
+                                   void* dbias, int dparam_dtype, int64_t rows, int64_t dim,
+                                   int dtype, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  const char* fn = "scree_layernorm_bwd";
+  int rc = validate_common(fn, rows, dim, dtype);
+  if (rc) return rc;
+  if (dweight && !weight) return set_error(SCREE_ERR_INVALID, "%s: dweight requires weight", fn);
+  if (rows == 0 && !dweight && !dbias) return SCREE_OK;
+  if (!mean) return set_error(SCREE_ERR_INVALID, "%s: mean must be non-null", fn);
+  rc = validate_bwd(fn, dy, x, rstd, dx, dweight != nullptr || dbias != nullptr, dparam_dtype, rows,
+                    dim, workspace, workspace_bytes);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32: return launch_bwd<float, true>(dy, x, weight, mean, rstd, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
+    case SCREE_DTYPE_F16: return launch_bwd<f16, true>(dy, x, weight, mean, rstd, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
+    default: return launch_bwd<bf16, true>(dy, x, weight, mean, rstd, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
+  }
+}

@@ -1,0 +1,56 @@
+"""Array-level varlen kernels on the HIP path.
+
+Same signatures as the reference's ``scree.kernels.reference`` functions
+(``src/scree/kernels/reference/varlen_attention.py:10``,
+``varlen_rmsnorm.py:18``, ``varlen_layernorm.py:14``), taking and returning
+:class:`scree_amd.Array`.  They run only on ROCm device tensors -- there is no
+CPU implementation here; a host array raises ``TypeError``.  Outputs reuse
+the input's offsets, as the reference does.
+"""
+
+from __future__ import annotations
+
+from .._core import Array, _is_torch
+
+
+def _require_device(values, fn: str) -> None:
+    if not (_is_torch(values) and values.is_cuda):
+        raise TypeError(f"{fn}: the HIP kernels need ROCm device tensors, got {type(values).__name__}"
+                        f"{' on ' + str(values.device) if _is_torch(values) else ''}")
+
+
+def varlen_attention(q: Array, k: Array, v: Array, causal: bool = False) -> Array:
+    """Per-sequence self-attention of packed ``(total, heads, head_dim)`` arrays."""
+    import torch
+
+    from .hip import varlen_attention_hip_autograd
+
+    _require_device(q.values, "varlen_attention")
+    if not (q.offsets is k.offsets and q.offsets is v.offsets):
+        if not (torch.equal(q.offsets, k.offsets) and torch.equal(q.offsets, v.offsets)):
+            raise ValueError("q, k, v must have identical offsets")
+    if q.ragged_dim != 0:
+        raise NotImplementedError("varlen_attention supports ragged_dim=0 only")
+    out = varlen_attention_hip_autograd(q.values, k.values, v.values, q.offsets, causal)
+    return Array(values=out, offsets=q.offsets, ragged_dim=0)
+
+
+def varlen_rmsnorm(arr: Array, weight=None, eps: float = 1e-6) -> Array:
+    """RMSNorm over the last axis of a packed array."""
+    from .hip import varlen_rmsnorm_hip
+
+    _require_device(arr.values, "varlen_rmsnorm")
+    return Array(values=varlen_rmsnorm_hip(arr.values, weight, eps), offsets=arr.offsets,
+                 ragged_dim=arr.ragged_dim)
+
+
+def varlen_layernorm(arr: Array, weight=None, bias=None, eps: float = 1e-5) -> Array:
+    """LayerNorm over the last axis of a packed array."""
+    from .hip import varlen_layernorm_hip
+
+    _require_device(arr.values, "varlen_layernorm")
+    return Array(values=varlen_layernorm_hip(arr.values, weight, bias, eps), offsets=arr.offsets,
+                 ragged_dim=arr.ragged_dim)
+
+
+__all__ = ["varlen_attention", "varlen_layernorm", "varlen_rmsnorm"]

@@ -1,0 +1,51 @@
+"""``torch.autograd.Function`` around the HIP attention forward and backward.
+
+Mirrors ``varlen_attention_triton_autograd``
+(``src/scree/kernels/triton/_autograd.py:17-72``): forward saves
+``(q, k, v, out, lse, cu_seqlens)`` and backward returns ``(dq, dk, dv, None,
+None)``.  Two differences: the Function class is defined once at import
+(the reference rebuilds it on every call, ``_autograd.py:71``), and the
+forward also keeps the device work list it built, so the backward launches
+no scheduler and never synchronises the host.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import attention as _attn
+
+
+class VarlenAttentionHip(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_seqlens, causal):
+        _attn._check_inputs(q, k, v)
+        total, n_heads, head_dim = q.shape
+        cu = _attn._cu(cu_seqlens, q.device)
+        qk, kk, vk = _attn._kernel_view(q), _attn._kernel_view(k), _attn._kernel_view(v)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        lse = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
+        with torch.cuda.device(q.device):
+            ws = _attn.attention_schedule(cu, total, head_dim, causal)
+            _attn._attn_fwd(qk, kk, vk, cu, causal, out, lse, ws)
+        ctx.save_for_backward(qk, kk, vk, out, lse, cu, ws)
+        ctx.causal = causal
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        q, k, v, out, lse, cu, ws = ctx.saved_tensors
+        do = _attn._kernel_view(grad_output)
+        dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+        dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+        dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+        total, n_heads, _ = q.shape
+        delta = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
+        with torch.cuda.device(q.device):
+            _attn._attn_bwd(do, q, k, v, out, lse, cu, ctx.causal, dq, dk, dv, delta, ws)
+        return dq, dk, dv, None, None
+
+
+def varlen_attention_hip_autograd(q, k, v, cu_seqlens, causal: bool = False):
+    """Autograd-aware varlen attention; ``out.backward()`` runs the HIP backward."""
+    return VarlenAttentionHip.apply(q, k, v, cu_seqlens, causal)

@@ -1,0 +1,186 @@
+"""Varlen self-attention on the HIP kernels: tensor-level launchers.
+
+Signatures and behaviour mirror the reference's Triton launchers so callers
+can switch by changing the import:
+
+* :func:`varlen_attention_hip` <- ``varlen_attention_triton``
+  (``src/scree/kernels/triton/varlen_attention.py:165-268``)
+* :func:`varlen_attention_hip_backward` <- ``varlen_attention_triton_backward``
+  (``src/scree/kernels/triton/_backward.py:288-396``)
+
+Differences a caller can observe:
+
+* ``block_m`` / ``block_n`` are accepted and ignored: tile shapes are fixed
+  per head_dim inside the library.
+* No host synchronisation: the reference reads ``max(seq_lens)`` with
+  ``.item()`` (``varlen_attention.py:220-221``); here a device scheduler turns
+  ``cu_seqlens`` into a work list (:func:`attention_schedule`).
+* head_dim must be 32, 64 or 128; q/k/v may be strided views whose last axis
+  is contiguous (other layouts are copied to contiguous first).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _ffi
+
+
+def _check_inputs(q, k, v):
+    assert q.shape == k.shape == v.shape, "q, k, v must have identical shape"
+    assert q.is_cuda, "varlen_attention_hip requires ROCm device tensors"
+    assert q.dtype in (torch.float16, torch.bfloat16), "fp16 or bf16 only"
+    assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
+    assert q.dim() == 3, "q, k, v must be (total_tokens, n_heads, head_dim)"
+
+
+def _kernel_view(t: torch.Tensor) -> torch.Tensor:
+    """``t`` itself when the library can read it in place, else a contiguous copy."""
+    ok = (
+        t.stride(2) == 1
+        and t.stride(0) % 8 == 0
+        and t.stride(1) % 8 == 0
+        and t.data_ptr() % 16 == 0
+        and (t.shape[0] <= 1 or t.stride(0) >= t.shape[2])
+    )
+    return t if ok else t.contiguous()
+
+
+def _cu(cu_seqlens: torch.Tensor, device) -> torch.Tensor:
+    cu = cu_seqlens
+    if cu.device != device:
+        cu = cu.to(device)
+    if cu.dtype != torch.int32:
+        cu = cu.to(torch.int32)
+    return cu.contiguous()
+
+
+def workspace_bytes(batch: int, total: int, head_dim: int) -> int:
+    return int(_ffi.lib().scree_attn_workspace_bytes(batch, total, head_dim))
+
+
+def attention_schedule(cu_seqlens: torch.Tensor, total_tokens: int, head_dim: int, causal: bool,
+                       workspace: torch.Tensor = None) -> torch.Tensor:
+    """Build the device work list for ``cu_seqlens`` and return its workspace.
+
+    The returned uint8 tensor can be passed as ``workspace=`` to the forward
+    and backward launchers for the same ``cu_seqlens``/``head_dim``/``causal``.
+    """
+    lib = _ffi.lib()
+    batch = cu_seqlens.numel() - 1
+    nbytes = workspace_bytes(batch, total_tokens, head_dim)
+    if workspace is None:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=cu_seqlens.device)
+    with torch.cuda.device(cu_seqlens.device):
+        _ffi.check(lib.scree_attn_schedule(
+            _ffi.ptr(cu_seqlens), batch, total_tokens, head_dim, int(bool(causal)),
+            _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(cu_seqlens)))
+    return workspace
+
+
+def schedule_items(workspace: torch.Tensor, with_ranges: bool = False):
+    """Decode a schedule workspace into ``(count, items)`` on the host (tests).
+
+    ``items`` is ``(count, 2)`` of ``(seq, blk)``, or ``(count, 4)`` with the
+    sequence's clamped ``(start, len)`` when ``with_ranges``.
+    """
+    header = workspace[:16].view(torch.int32).cpu()
+    count = int(header[0])
+    items = workspace[16:16 + 16 * count].view(torch.int32).reshape(-1, 4).cpu()
+    return count, (items if with_ranges else items[:, :2].contiguous())
+
+
+def _attn_fwd(q, k, v, cu, causal, out, lse, workspace):
+    lib = _ffi.lib()
+    total, heads, head_dim = q.shape
+    strides = _ffi.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+                                v.stride(0), v.stride(1), out.stride(0), out.stride(1)])
+    _ffi.check(lib.scree_attn_fwd(
+        _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(out), _ffi.ptr(lse), _ffi.ptr(cu),
+        cu.numel() - 1, total, heads, head_dim, strides, 1.0 / math.sqrt(head_dim),
+        int(bool(causal)), _ffi.dtype_code(q.dtype), _ffi.ptr(workspace), workspace.numel(),
+        _ffi.stream_of(q)))
+
+
+def _attn_bwd(do, q, k, v, o, lse, cu, causal, dq, dk, dv, delta, workspace):
+    lib = _ffi.lib()
+    total, heads, head_dim = q.shape
+    ts = (do, q, k, v, o, dq, dk, dv)
+    strides = _ffi.int64_array([s for t in ts for s in (t.stride(0), t.stride(1))])
+    _ffi.check(lib.scree_attn_bwd(
+        _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(o), _ffi.ptr(lse),
+        _ffi.ptr(dq), _ffi.ptr(dk), _ffi.ptr(dv), _ffi.ptr(delta), _ffi.ptr(cu),
+        cu.numel() - 1, total, heads, head_dim, strides, 1.0 / math.sqrt(head_dim),
+        int(bool(causal)), _ffi.dtype_code(q.dtype), _ffi.ptr(workspace), workspace.numel(),
+        _ffi.stream_of(q)))
+
+
+def varlen_attention_hip(q, k, v, cu_seqlens, causal: bool = False, block_m: int = 64,
+                         block_n: int = 64, return_lse: bool = False, out=None, lse_buffer=None,
+                         workspace=None):
+    """Variable-length self-attention forward on the HIP kernels.
+
+    Parameters follow ``varlen_attention_triton``: ``q, k, v`` are
+    ``(total_tokens, n_heads, head_dim)`` fp16/bf16 device tensors,
+    ``cu_seqlens`` the int32 ``(batch + 1,)`` offsets.  ``out`` /
+    ``lse_buffer`` are optional preallocated outputs.  ``workspace`` is an
+    optional schedule from :func:`attention_schedule` for these offsets.
+
+    Returns ``out`` or ``(out, lse)`` with ``lse`` the natural-log
+    logsumexp of the scaled scores, ``(total_tokens, n_heads)`` fp32.
+    """
+    del block_m, block_n  # tile shapes are fixed inside the library
+    _check_inputs(q, k, v)
+    total, n_heads, head_dim = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        assert out.shape == q.shape and out.dtype == q.dtype and out.device == q.device
+    if lse_buffer is None:
+        lse = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
+    else:
+        assert lse_buffer.shape == (total, n_heads)
+        assert lse_buffer.dtype == torch.float32 and lse_buffer.device == q.device
+        assert lse_buffer.is_contiguous(), "lse_buffer must be contiguous"
+        lse = lse_buffer
+    cu = _cu(cu_seqlens, q.device)
+    qk, kk, vk = _kernel_view(q), _kernel_view(k), _kernel_view(v)
+    ok = _kernel_view(out)
+    with torch.cuda.device(q.device):
+        if workspace is None:
+            workspace = attention_schedule(cu, total, head_dim, causal)
+        _attn_fwd(qk, kk, vk, cu, causal, ok, lse, workspace)
+    if ok is not out:
+        out.copy_(ok)
+    if return_lse:
+        return out, lse
+    return out
+
+
+def varlen_attention_hip_backward(do, q, k, v, o, lse, cu_seqlens, causal: bool = False,
+                                  block_m: int = 64, block_n: int = 64, workspace=None,
+                                  delta_buffer=None):
+    """``(dq, dk, dv)`` for varlen self-attention; mirrors ``varlen_attention_triton_backward``.
+
+    ``lse`` is the forward's logsumexp.  ``delta_buffer`` (optional,
+    ``(total, heads)`` fp32) receives ``rowsum(o * do)``.
+    """
+    del block_m, block_n
+    _check_inputs(q, k, v)
+    assert do.shape == q.shape and o.shape == q.shape, "do and o must match q"
+    total, n_heads, head_dim = q.shape
+    assert lse.shape == (total, n_heads) and lse.dtype == torch.float32
+    cu = _cu(cu_seqlens, q.device)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    delta = delta_buffer if delta_buffer is not None else torch.empty(
+        (total, n_heads), dtype=torch.float32, device=q.device)
+    ins = [_kernel_view(t) for t in (do, q, k, v, o)]
+    with torch.cuda.device(q.device):
+        if workspace is None:
+            workspace = attention_schedule(cu, total, head_dim, causal)
+        _attn_bwd(*ins, lse.contiguous(), cu, causal, dq, dk, dv, delta, workspace)
+    return dq, dk, dv

@@ -1,0 +1,123 @@
+"""The C-ABI library: it loads, exports every function ``include/scree_hip.h``
+declares, and rejects bad arguments on the host (no GPU needed: every call here
+fails validation before anything is launched)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from scree_amd.kernels.hip import _ffi
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "scree_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(scree_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads():
+    assert _ffi.HIP_AVAILABLE, f"library failed to load from {_ffi.library_path()}"
+    assert _ffi.lib().scree_abi_version() == 1
+
+
+def test_exports_every_declared_symbol():
+    declared = _declared()
+    assert declared, "no declarations parsed from the header"
+    raw = ctypes.CDLL(str(_ffi.library_path()))
+    for name in declared:
+        assert hasattr(raw, name), f"{name} declared in scree_hip.h but not exported"
+    assert sorted(_ffi.EXPORTED) == declared
+
+
+def _err():
+    return _ffi.lib().scree_last_error().decode()
+
+
+def test_attention_validation_errors():
+    lib = _ffi.lib()
+    ws = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.c_void_p(ctypes.addressof(ws))
+    strides = _ffi.int64_array([16 * 64, 64] * 8)
+    null = ctypes.c_void_p(0)
+    # null cu_seqlens
+    rc = lib.scree_attn_fwd(p, p, p, p, p, null, 2, 10, 16, 64, strides, 0.125, 1, 1, p, 1 << 16, null)
+    assert rc == _ffi.SCREE_ERR_INVALID and "cu_seqlens" in _err()
+    # unsupported head_dim
+    rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 48, strides, 0.125, 1, 1, p, 1 << 16, null)
+    assert rc == _ffi.SCREE_ERR_UNSUPPORTED and "head_dim" in _err()
+    # fp32 is not an attention dtype
+    rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 64, strides, 0.125, 1, 0, p, 1 << 16, null)
+    assert rc == _ffi.SCREE_ERR_UNSUPPORTED and "dtype" in _err()
+    # workspace too small
+    rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 64, strides, 0.125, 1, 1, p, 8, null)
+    assert rc == _ffi.SCREE_ERR_WORKSPACE
+    # stride not a multiple of 8 elements
+    bad = _ffi.int64_array([16 * 64 + 4, 64] * 8)
+    rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 64, bad, 0.125, 1, 1, p, 1 << 16, null)
+    assert rc == _ffi.SCREE_ERR_INVALID and "strides" in _err()
+    # batch out of range
+    rc = lib.scree_attn_schedule(p, 0, 10, 64, 1, p, 1 << 16, null)
+    assert rc == _ffi.SCREE_ERR_UNSUPPORTED
+    rc = lib.scree_attn_bwd(p, p, p, p, p, p, p, p, p, null, p, 2, 10, 16, 64, strides, 0.125, 1, 1,
+                            p, 1 << 16, null)
+    assert rc == _ffi.SCREE_ERR_INVALID and "delta" in _err()
+
+
+def test_workspace_sizes():
+    lib = _ffi.lib()
+    # header + (ceil(N/128) + B) int4 items
+    assert lib.scree_attn_workspace_bytes(16, 12160, 64) == 16 + 16 * (95 + 16)
+    assert lib.scree_attn_workspace_bytes(0, 10, 64) == 0
+    assert lib.scree_norm_bwd_workspace_bytes(19758, 4096) == 512 * 2 * 4096 * 4
+    assert lib.scree_norm_bwd_workspace_bytes(10, 100) == 2 * 2 * 100 * 4
+
+
+def test_norm_validation_errors():
+    lib = _ffi.lib()
+    null = ctypes.c_void_p(0)
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.c_void_p(ctypes.addressof(buf))
+    assert lib.scree_rmsnorm_fwd(null, null, null, null, 4, 8, 1e-6, 1, null) == _ffi.SCREE_ERR_INVALID
+    assert lib.scree_rmsnorm_fwd(p, null, p, null, 4, 0, 1e-6, 1, null) == _ffi.SCREE_ERR_INVALID
+    assert "dim" in _err()
+    assert lib.scree_layernorm_fwd(p, null, null, p, null, null, 4, 8, 1e-6, 7, null) == _ffi.SCREE_ERR_UNSUPPORTED
+    # nothing to do for zero rows
+    assert lib.scree_rmsnorm_fwd(null, null, null, null, 0, 8, 1e-6, 1, null) == _ffi.SCREE_OK
+    # dweight without weight
+    rc = lib.scree_rmsnorm_bwd(p, p, null, p, p, p, 0, 4, 8, 1, p, 256, null)
+    assert rc == _ffi.SCREE_ERR_INVALID and "dweight" in _err()
+    # workspace too small for the parameter gradient
+    rc = lib.scree_layernorm_bwd(p, p, p, p, p, p, p, null, 0, 4, 8, 1, p, 4, null)
+    assert rc == _ffi.SCREE_ERR_WORKSPACE
+
+
+def test_python_errors_map_codes():
+    with pytest.raises(ValueError):
+        _ffi.check(_ffi.lib().scree_rmsnorm_fwd(None, None, None, None, 4, 8, 1e-6, 1, None))
+    with pytest.raises(NotImplementedError):
+        _ffi.check(_ffi.lib().scree_rmsnorm_fwd(None, None, None, None, 4, 8, 1e-6, 9, None))
+
+
+def test_cpu_tensors_are_rejected_by_the_hip_path():
+    import numpy as np
+    import torch
+
+    import scree_amd as scree
+    from scree_amd.kernels import varlen_attention, varlen_rmsnorm
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_rmsnorm_hip
+
+    x = torch.zeros(4, 2, 32, dtype=torch.float16)
+    cu = torch.tensor([0, 4], dtype=torch.int32)
+    with pytest.raises(AssertionError, match="ROCm"):
+        varlen_attention_hip(x, x, x, cu)
+    with pytest.raises(AssertionError, match="ROCm"):
+        varlen_rmsnorm_hip(torch.zeros(4, 8))
+    arr = scree.pack([np.zeros((3, 8), dtype=np.float32)])
+    with pytest.raises(TypeError, match="ROCm"):
+        varlen_rmsnorm(arr)
+    with pytest.raises(TypeError, match="ROCm"):
+        varlen_attention(arr, arr, arr)

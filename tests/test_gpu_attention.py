@@ -1,0 +1,219 @@
+"""GPU parity of the HIP attention kernels against the oracle.
+
+Every case prints its name before touching the GPU.  Inputs are seeded,
+rounded to the kernel dtype, and the oracle runs in fp64 on those rounded
+values.  Tolerances: see ``tests/parity.py``.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import attention_bwd, attention_fwd
+from oracle.schedule import build_schedule
+from parity import UNIT, attn_abs_terms, check_close, cu_of, np64, randn, say
+from scree_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+EDGE_LENGTHS = [1, 63, 64, 65, 127, 128, 129, 255, 300, 2]
+
+
+def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True):
+    say(f"case: lengths[:6]={lengths[:6]} B={len(lengths)} N={sum(lengths)} H={heads} D={dim} "
+        f"{dtype} causal={causal}")
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
+
+    n = sum(lengths)
+    off, cu = cu_of(lengths)
+    q = randn((n, heads, dim), dtype, seed)
+    k = randn((n, heads, dim), dtype, seed + 1)
+    v = randn((n, heads, dim), dtype, seed + 2)
+    out, lse = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    q64, k64, v64 = np64(q), np64(k), np64(v)
+    ref_o, ref_lse = attention_fwd(q64, k64, v64, off, causal=causal)
+    u = UNIT[dtype]
+    bf16 = dtype == torch.bfloat16
+    do = randn((n, heads, dim), dtype, seed + 3) if backward else None
+    do64 = np64(do) if backward else None
+    terms = attn_abs_terms(q64, k64, v64, do64, ref_lse, off, causal) if bf16 else None
+    check_close("O", np64(out), ref_o, 2e-3,
+                extra=(2 * terms[0] + np.abs(ref_o)) if bf16 else None, unit=u)
+    check_close("LSE", lse.cpu().numpy().astype(np.float64), ref_lse, 1e-4 + 1e-5 * np.abs(ref_lse).max())
+    if not backward:
+        return
+    dq, dk, dv = varlen_attention_hip_backward(do, q, k, v, out, lse, cu, causal=causal)
+    torch.cuda.synchronize()
+    rdq, rdk, rdv, _ = attention_bwd(do64, q64, k64, v64, np64(out), ref_lse, off, causal=causal)
+    check_close("dQ", np64(dq), rdq, 5e-3, extra=(2 * terms[2] + np.abs(rdq)) if bf16 else None, unit=u)
+    check_close("dK", np64(dk), rdk, 5e-3, extra=(2 * terms[3] + np.abs(rdk)) if bf16 else None, unit=u)
+    check_close("dV", np64(dv), rdv, 5e-3, extra=(2 * terms[1] + np.abs(rdv)) if bf16 else None, unit=u)
+
+
+@pytest.mark.parametrize("dim", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_edge_lengths(dim, dtype, causal):
+    _run_case(EDGE_LENGTHS, 2, dim, dtype, causal, seed=dim)
+
+
+def test_single_token_sequences():
+    _run_case([1, 1, 1, 1], 3, 64, torch.float16, True)
+
+
+def test_empty_sequences_in_batch():
+    _run_case([0, 70, 0, 0, 130, 0], 2, 64, torch.float16, True)
+
+
+def test_config3_fixed_list_fp16_causal():
+    c = workloads.config3(fixed=True)
+    _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=3)
+
+
+def test_config3_rescaled_lengths_fp16_causal():
+    c = workloads.config3()
+    _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=4, backward=False)
+
+
+def test_config5_sampled_heads_bf16():
+    """Config 5 shape on the GPU; the oracle checks two heads of four sequences
+    (including the longest, 10555 tokens) -- heads are independent."""
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
+
+    c = workloads.config5()
+    say(f"case: config5 N={c.total} H={c.heads} D={c.head_dim} bf16 causal")
+    n, h, d = c.total, c.heads, c.head_dim
+    off, cu = cu_of(c.lengths)
+    q = randn((n, h, d), torch.bfloat16, 50)
+    k = randn((n, h, d), torch.bfloat16, 51)
+    v = randn((n, h, d), torch.bfloat16, 52)
+    do = randn((n, h, d), torch.bfloat16, 53)
+    out, lse = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    dq, dk, dv = varlen_attention_hip_backward(do, q, k, v, out, lse, cu, causal=True)
+    torch.cuda.synchronize()
+    longest = int(np.argmax(c.lengths))
+    picks = sorted({longest, int(np.argmin(c.lengths)), 0, 5})
+    heads = [0, 17]
+    u = UNIT[torch.bfloat16]
+    for s in picks:
+        a, b = int(off[s]), int(off[s + 1])
+        say(f"  seq {s} len {b - a} heads {heads}")
+        sl = (slice(a, b), heads)
+        sub = lambda t: np64(t[a:b][:, heads])  # noqa: E731
+        q64, k64, v64, do64 = sub(q), sub(k), sub(v), sub(do)
+        loff = np.array([0, b - a], dtype=np.int32)
+        ro, rl = attention_fwd(q64, k64, v64, loff, causal=True, dtype=np.float64)
+        terms = attn_abs_terms(q64, k64, v64, do64, rl, loff, True)
+        check_close("O", sub(out), ro, 2e-3, extra=2 * terms[0] + np.abs(ro), unit=u)
+        check_close("LSE", lse[a:b][:, heads].cpu().numpy().astype(np.float64), rl, 1e-4 + 1e-5 * np.abs(rl).max())
+        rdq, rdk, rdv, _ = attention_bwd(do64, q64, k64, v64, sub(out), rl, loff, causal=True)
+        check_close("dQ", sub(dq), rdq, 5e-3, extra=2 * terms[2] + np.abs(rdq), unit=u)
+        check_close("dK", sub(dk), rdk, 5e-3, extra=2 * terms[3] + np.abs(rdk), unit=u)
+        check_close("dV", sub(dv), rdv, 5e-3, extra=2 * terms[1] + np.abs(rdv), unit=u)
+        del sl
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_schedule_bit_exact(causal):
+    from scree_amd.kernels.hip import attention_schedule, schedule_items
+
+    cases = [EDGE_LENGTHS, [5], [0, 0, 3], workloads.config3().lengths,
+             workloads.config5().lengths, list(range(1, 2049)), [600000, 5, 200]]
+    for lengths in cases:
+        say(f"case: schedule B={len(lengths)} N={sum(lengths)} causal={causal}")
+        off, cu = cu_of(lengths)
+        ws = attention_schedule(cu, int(sum(lengths)), 64, causal)
+        count, items = schedule_items(ws)
+        want = build_schedule(off, 128, causal)
+        assert count == len(want)
+        np.testing.assert_array_equal(items.numpy(), want)
+
+
+def test_strided_qkv_views_match_contiguous():
+    from scree_amd.kernels.hip import varlen_attention_hip
+
+    say("case: strided qkv views")
+    lengths = [70, 33, 190]
+    n = sum(lengths)
+    _, cu = cu_of(lengths)
+    qkv = randn((n, 3, 4, 64), torch.float16, 7)
+    q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    assert not q.is_contiguous()
+    a, la = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    b, lb = varlen_attention_hip(q.contiguous(), k.contiguous(), v.contiguous(), cu, causal=True,
+                                 return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+def test_deterministic_forward_and_backward():
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
+
+    say("case: determinism")
+    lengths = [300, 17, 129]
+    n = sum(lengths)
+    _, cu = cu_of(lengths)
+    q, k, v, do = (randn((n, 4, 64), torch.bfloat16, s) for s in range(4))
+    o1, l1 = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    o2, l2 = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    g1 = varlen_attention_hip_backward(do, q, k, v, o1, l1, cu, causal=True)
+    g2 = varlen_attention_hip_backward(do, q, k, v, o2, l2, cu, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_autograd_wrapper_matches_explicit_backward():
+    from scree_amd.kernels.hip import (varlen_attention_hip, varlen_attention_hip_autograd,
+                                       varlen_attention_hip_backward)
+
+    say("case: autograd wrapper")
+    lengths = [64, 200, 3]
+    n = sum(lengths)
+    _, cu = cu_of(lengths)
+    q, k, v, do = (randn((n, 2, 128), torch.float16, 10 + s) for s in range(4))
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = varlen_attention_hip_autograd(qa, ka, va, cu, causal=True)
+    out.backward(do)
+    o, lse = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    dq, dk, dv = varlen_attention_hip_backward(do, q, k, v, o, lse, cu, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.detach(), o)
+    assert torch.equal(qa.grad, dq) and torch.equal(ka.grad, dk) and torch.equal(va.grad, dv)
+
+
+def test_preallocated_out_and_lse_buffers():
+    from scree_amd.kernels.hip import varlen_attention_hip
+
+    say("case: out= / lse_buffer=")
+    lengths = [40, 90]
+    n = sum(lengths)
+    _, cu = cu_of(lengths)
+    q, k, v = (randn((n, 2, 32), torch.float16, 20 + s) for s in range(3))
+    out = torch.empty_like(q)
+    lse = torch.empty((n, 2), dtype=torch.float32, device="cuda")
+    r = varlen_attention_hip(q, k, v, cu, causal=False, return_lse=True, out=out, lse_buffer=lse)
+    torch.cuda.synchronize()
+    assert r[0] is out and r[1] is lse
+    o2 = varlen_attention_hip(q, k, v, cu, causal=False)
+    assert torch.equal(o2, out)
+
+
+def test_array_level_api_on_device():
+    import scree_amd as scree
+    from scree_amd.kernels import varlen_attention
+
+    say("case: Array-level varlen_attention")
+    seqs = [randn((n, 2, 64), torch.float16, n) for n in (5, 77, 130)]
+    q = scree.pack(seqs)
+    out = varlen_attention(q, q, q, causal=True)
+    torch.cuda.synchronize()
+    assert out.offsets is q.offsets
+    off = q.offsets.cpu().numpy()
+    ref, _ = attention_fwd(np64(q.values), np64(q.values), np64(q.values), off, causal=True)
+    check_close("O", np64(out.values), ref, 2e-3)
+    other = scree.pack([randn((n, 2, 64), torch.float16, 1) for n in (6, 76, 130)])
+    with pytest.raises(ValueError, match="identical offsets"):
+        varlen_attention(q, other, other)

@@ -1,0 +1,214 @@
+"""Pins the attention oracle (forward, LSE, backward) before it is trusted.
+
+* the reference's own known-answer tests (``tests/test_varlen_kernels.py:19-75``
+  and ``tests/test_autograd.py:67-78``), restated;
+* brute force with explicit Python loops in fp64 on tiny inputs;
+* ``torch.nn.functional.scaled_dot_product_attention`` per sequence, and torch
+  autograd through it for the backward;
+* fp64 central finite differences of the backward;
+* invariants: rows of exp(S - LSE) sum to 1, sum_k dS = 0, identical keys
+  average the values.
+A dropped term, wrong sign, transposed operand or misplaced mask fails at
+least one of these.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.attention import attention_bwd, attention_fwd, attention_lse
+from oracle.core import offsets_from_lengths
+
+
+def _inputs(lengths, heads, dim, seed=0):
+    rng = np.random.default_rng(seed)
+    n = sum(lengths)
+    q = rng.standard_normal((n, heads, dim))
+    k = rng.standard_normal((n, heads, dim))
+    v = rng.standard_normal((n, heads, dim))
+    return q, k, v, offsets_from_lengths(lengths)
+
+
+def _brute(q, k, v, off, causal):
+    n, h, d = q.shape
+    out = np.zeros_like(q)
+    lse = np.zeros((n, h))
+    for b in range(len(off) - 1):
+        s, e = off[b], off[b + 1]
+        for hh in range(h):
+            for i in range(s, e):
+                keys = range(s, i + 1) if causal else range(s, e)
+                sc = [sum(q[i, hh, t] * k[j, hh, t] for t in range(d)) / math.sqrt(d) for j in keys]
+                m = max(sc)
+                w = [math.exp(x - m) for x in sc]
+                z = sum(w)
+                lse[i, hh] = m + math.log(z)
+                for t in range(d):
+                    out[i, hh, t] = sum(wj * v[j, hh, t] for wj, j in zip(w, keys)) / z
+    return out, lse
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_matches_brute_force(causal):
+    q, k, v, off = _inputs([3, 1, 5, 2], 2, 4)
+    want_o, want_l = _brute(q, k, v, off, causal)
+    for impl in ("einsum", "matmul"):
+        o, lse = attention_fwd(q, k, v, off, causal=causal, impl=impl)
+        np.testing.assert_allclose(o, want_o, atol=1e-12)
+        np.testing.assert_allclose(lse, want_l, atol=1e-12)
+
+
+def test_reference_known_answer_per_sequence_baseline():
+    # reference tests/test_varlen_kernels.py:19-43
+    rng = np.random.default_rng(0)
+    n_heads, head_dim, lengths = 2, 4, [3, 5, 2]
+    sq = [rng.standard_normal((n, n_heads, head_dim)).astype(np.float32) for n in lengths]
+    sk = [rng.standard_normal((n, n_heads, head_dim)).astype(np.float32) for n in lengths]
+    sv = [rng.standard_normal((n, n_heads, head_dim)).astype(np.float32) for n in lengths]
+    off = offsets_from_lengths(lengths)
+    o, _ = attention_fwd(np.concatenate(sq), np.concatenate(sk), np.concatenate(sv), off,
+                         causal=False, dtype=np.float32, impl="einsum")
+    for i in range(len(lengths)):
+        scores = np.einsum("ihd,jhd->hij", sq[i], sk[i]) / np.sqrt(head_dim)
+        attn = np.exp(scores - scores.max(-1, keepdims=True))
+        attn /= attn.sum(-1, keepdims=True)
+        base = np.einsum("hij,jhd->ihd", attn, sv[i])
+        np.testing.assert_allclose(o[off[i]:off[i + 1]], base, atol=1e-5)
+
+
+def test_reference_known_answer_causal_first_token_is_v0():
+    # reference tests/test_varlen_kernels.py:46-63
+    q, k, v, off = _inputs([4, 6], 1, 4)
+    o, _ = attention_fwd(q, k, v, off, causal=True)
+    for i in range(2):
+        np.testing.assert_allclose(o[off[i]], v[off[i]], atol=1e-12)
+
+
+def test_rejects_mismatched_offsets():
+    # reference tests/test_varlen_kernels.py:66-75
+    q, k, v, off = _inputs([3, 5], 1, 4)
+    with pytest.raises(ValueError, match=r"identical offsets"):
+        attention_fwd(q, k, v, off, k_offsets=offsets_from_lengths([4, 4]))
+
+
+def test_length_one_sequences():
+    # reference tests/test_autograd.py:67-78: length-1 rows attend to themselves only
+    q, k, v, off = _inputs([1, 1, 1], 2, 8)
+    for causal in (False, True):
+        o, lse = attention_fwd(q, k, v, off, causal=causal)
+        np.testing.assert_allclose(o, v, atol=1e-12)
+        np.testing.assert_allclose(lse, (q * k).sum(-1) / math.sqrt(8), atol=1e-12)
+
+
+def test_identical_keys_average_values():
+    lengths = [7]
+    q, k, v, off = _inputs(lengths, 1, 4)
+    k[:] = k[0]
+    o, _ = attention_fwd(q, k, v, off, causal=False)
+    np.testing.assert_allclose(o, np.broadcast_to(v.mean(0), o.shape), atol=1e-12)
+    oc, _ = attention_fwd(q, k, v, off, causal=True)
+    for i in range(7):
+        np.testing.assert_allclose(oc[i], v[: i + 1].mean(0), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_matches_torch_sdpa(causal):
+    lengths = [17, 1, 64, 33, 90]
+    q, k, v, off = _inputs(lengths, 3, 16, seed=1)
+    o, lse = attention_fwd(q, k, v, off, causal=causal)
+    for b in range(len(lengths)):
+        s, e = off[b], off[b + 1]
+        tq, tk, tv = (torch.from_numpy(x[s:e]).permute(1, 0, 2) for x in (q, k, v))
+        ref = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal).permute(1, 0, 2)
+        np.testing.assert_allclose(o[s:e], ref.numpy(), atol=1e-10)
+        sc = torch.einsum("hid,hjd->hij", tq, tk) / math.sqrt(16)
+        if causal:
+            sc = sc.masked_fill(torch.triu(torch.ones(e - s, e - s, dtype=torch.bool), 1), -math.inf)
+        np.testing.assert_allclose(lse[s:e], torch.logsumexp(sc, -1).T.numpy(), atol=1e-10)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_lse_independent_and_normalises(causal):
+    lengths = [9, 20, 3]
+    q, k, v, off = _inputs(lengths, 2, 8, seed=2)
+    _, lse = attention_fwd(q, k, v, off, causal=causal)
+    np.testing.assert_allclose(lse, attention_lse(q, k, off, causal=causal), atol=1e-12)
+    for b in range(len(lengths)):
+        s, e = off[b], off[b + 1]
+        sc = np.einsum("ihd,jhd->hij", q[s:e], k[s:e]) / math.sqrt(8)
+        if causal:
+            sc = np.where(np.triu(np.ones((e - s, e - s), bool), 1), -np.inf, sc)
+        rows = np.exp(sc - lse[s:e].T[:, :, None]).sum(-1)
+        np.testing.assert_allclose(rows, 1.0, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_matches_torch_autograd(causal):
+    lengths = [5, 12, 1, 30]
+    q, k, v, off = _inputs(lengths, 2, 8, seed=3)
+    do = np.random.default_rng(9).standard_normal(q.shape)
+    o, lse = attention_fwd(q, k, v, off, causal=causal)
+    dq, dk, dv, delta = attention_bwd(do, q, k, v, o, lse, off, causal=causal)
+    np.testing.assert_allclose(delta, (o * do).sum(-1), atol=1e-12)
+    for b in range(len(lengths)):
+        s, e = off[b], off[b + 1]
+        tq, tk, tv = (torch.from_numpy(x[s:e]).permute(1, 0, 2).clone().requires_grad_(True)
+                      for x in (q, k, v))
+        out = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal)
+        out.backward(torch.from_numpy(do[s:e]).permute(1, 0, 2))
+        np.testing.assert_allclose(dq[s:e], tq.grad.permute(1, 0, 2).numpy(), atol=1e-10)
+        np.testing.assert_allclose(dk[s:e], tk.grad.permute(1, 0, 2).numpy(), atol=1e-10)
+        np.testing.assert_allclose(dv[s:e], tv.grad.permute(1, 0, 2).numpy(), atol=1e-10)
+    # einsum path agrees with matmul path
+    dq2, dk2, dv2, _ = attention_bwd(do, q, k, v, o, lse, off, causal=causal, impl="einsum")
+    np.testing.assert_allclose(dq2, dq, atol=1e-12)
+    np.testing.assert_allclose(dk2, dk, atol=1e-12)
+    np.testing.assert_allclose(dv2, dv, atol=1e-12)
+
+
+def test_backward_finite_differences():
+    lengths = [4, 3]
+    q, k, v, off = _inputs(lengths, 1, 3, seed=4)
+    do = np.random.default_rng(5).standard_normal(q.shape)
+
+    def loss(q_, k_, v_):
+        o_, _ = attention_fwd(q_, k_, v_, off, causal=True)
+        return float((o_ * do).sum())
+
+    o, lse = attention_fwd(q, k, v, off, causal=True)
+    grads = attention_bwd(do, q, k, v, o, lse, off, causal=True)[:3]
+    eps = 1e-6
+    for which, g in enumerate(grads):
+        base = [q, k, v]
+        for idx in [(0, 0, 0), (2, 0, 1), (3, 0, 2), (5, 0, 0), (6, 0, 1)]:
+            plus = [x.copy() for x in base]
+            minus = [x.copy() for x in base]
+            plus[which][idx] += eps
+            minus[which][idx] -= eps
+            fd = (loss(*plus) - loss(*minus)) / (2 * eps)
+            assert abs(fd - g[idx]) < 1e-7, (which, idx, fd, g[idx])
+
+
+def test_softmax_gradient_rows_sum_to_zero():
+    lengths = [11]
+    q, k, v, off = _inputs(lengths, 1, 4, seed=6)
+    do = np.random.default_rng(7).standard_normal(q.shape)
+    o, lse = attention_fwd(q, k, v, off, causal=True)
+    _, _, _, delta = attention_bwd(do, q, k, v, o, lse, off, causal=True)
+    sc = np.einsum("ihd,jhd->hij", q, k) / 2.0
+    sc = np.where(np.triu(np.ones((11, 11), bool), 1), -np.inf, sc)
+    p = np.exp(sc - lse.T[:, :, None])
+    dp = np.einsum("ihd,jhd->hij", do, v)
+    ds = p * (dp - delta.T[:, :, None])
+    np.testing.assert_allclose(ds.sum(-1), 0.0, atol=1e-12)
+
+
+def test_empty_sequence_is_skipped():
+    q, k, v, off = _inputs([3, 0, 2], 1, 4)
+    o, lse = attention_fwd(q, k, v, off, causal=True)
+    o2, lse2 = attention_fwd(q, k, v, offsets_from_lengths([3, 2]), causal=True)
+    np.testing.assert_array_equal(o, o2)
+    np.testing.assert_array_equal(lse, lse2)
