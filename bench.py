@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Throughput of the HIP varlen kernel path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]``
+
+Primary line: causal varlen attention forward +
+backward, fp16, 16 sequences summing to 12160 tokens (log-normal, sigma 0.6,
+rescaled), 16 heads x head_dim 64, synthetic N(0,1) inputs already resident
+in HBM.  One step = tile scheduler + forward (O, LSE) + dQ/Delta pass + dK/dV
+pass into preallocated buffers.  ``value`` is real-token causal TFLOP/s
+(4*H*D*sum L(L+1)/2 forward, x3.5 for forward+backward).
+
+Also reported (``secondary``): config 3 forward, config 4 on the reference's
+fixed H100 length list, config 5 (bf16, 32x128) forward+backward, config 2
+RMSNorm / LayerNorm forward and backward GB/s, the user-facing autograd step,
+and per-kernel HIP-event timings.  ``roofline`` describes the dominant kernel
+of the primary step; ``cpu_baseline`` times the numpy oracle (the reference's
+einsum call pattern) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_F16_TFLOPS = 2516.6   # MI355X dense fp16/bf16 MFMA, published
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _events_time(fn, reps: int) -> float:
+    """Average milliseconds of ``fn`` over ``reps`` back-to-back calls (HIP events)."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+class AttnCase:
+    """Preallocated tensors and the four launches of one attention step."""
+
+    def __init__(self, cfg, dtype, seed=0):
+        import numpy as np
+        import torch
+
+        from scree_amd.kernels.hip import attention as A
+
+        self.cfg, self.A = cfg, A
+        dev = torch.device("cuda:0")
+        n, h, d = cfg.total, cfg.heads, cfg.head_dim
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.q, self.k, self.v, self.do = (torch.randn(n, h, d, device=dev, dtype=dtype, generator=g)
+                                           for _ in range(4))
+        off = np.zeros(len(cfg.lengths) + 1, dtype=np.int32)
+        off[1:] = np.cumsum(cfg.lengths)
+        self.cu = torch.from_numpy(off).to(dev)
+        self.out = torch.empty_like(self.q)
+        self.lse = torch.empty(n, h, device=dev, dtype=torch.float32)
+        self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
+        self.delta = torch.empty(n, h, device=dev, dtype=torch.float32)
+        self.ws = torch.empty(A.workspace_bytes(len(cfg.lengths), n, d), dtype=torch.uint8, device=dev)
+
+    def schedule(self):
+        self.A.attention_schedule(self.cu, self.cfg.total, self.cfg.head_dim, self.cfg.causal, self.ws)
+
+    def fwd(self):
+        self.A._attn_fwd(self.q, self.k, self.v, self.cu, self.cfg.causal, self.out, self.lse, self.ws)
+
+    def bwd_dq(self):
+        self.A._attn_bwd_dq(self.do, self.q, self.k, self.v, self.out, self.lse, self.cu,
+                            self.cfg.causal, self.dq, self.delta, self.ws)
+
+    def bwd_dkv(self):
+        self.A._attn_bwd_dkv(self.do, self.q, self.k, self.v, self.lse, self.delta, self.cu,
+                             self.cfg.causal, self.dk, self.dv, self.ws)
+
+    def step_fwd(self):
+        self.schedule()
+        self.fwd()
+
+    def step_fwd_bwd(self):
+        self.schedule()
+        self.fwd()
+        self.bwd_dq()
+        self.bwd_dkv()
+
+
+def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False):
+    import torch
+
+    case = AttnCase(cfg, dtype)
+    step = case.step_fwd_bwd if backward else case.step_fwd
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = cfg.fwd_flops() * (3.5 if backward else 1.0)
+    res = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+    res["mfma_frac"] = res["tflops"] / PEAK_F16_TFLOPS
+    if per_kernel:
+        kernels = {"attn_schedule": case.schedule, "attn_fwd": case.fwd}
+        if backward:
+            kernels.update({"attn_bwd_dq": case.bwd_dq, "attn_bwd_dkv": case.bwd_dkv})
+        res["kernels_ms"] = {k: _events_time(f, max(steps, 10)) for k, f in kernels.items()}
+    return res, case
+
+
+def time_norms(cfg, steps, warmup):
+    import torch
+
+    from scree_amd import workloads
+    from scree_amd.kernels.hip import norms as Nm
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(2)
+    rows, dim = cfg.total, cfg.hidden
+    dt = torch.bfloat16
+    x = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+    w = (1 + 0.02 * torch.randn(dim, device=dev, generator=g)).to(dt)
+    b = (0.02 * torch.randn(dim, device=dev, generator=g)).to(dt)
+    dy = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+    _, rstd = Nm.rmsnorm_fwd(x, w, cfg.eps, True)
+    _, mean, lrstd = Nm.layernorm_fwd(x, w, b, cfg.eps, True)
+    fb = workloads.norm_fwd_bytes(rows, dim, 2, False)
+    bb = workloads.norm_bwd_bytes(rows, dim, 2, False)
+    lfb = workloads.norm_fwd_bytes(rows, dim, 2, True)
+    lbb = workloads.norm_bwd_bytes(rows, dim, 2, True)
+    cases = {
+        "rmsnorm_fwd": (lambda: Nm.rmsnorm_fwd(x, w, cfg.eps, True), fb),
+        "rmsnorm_bwd": (lambda: Nm.rmsnorm_bwd(dy, x, w, rstd, True, dw_like=w), bb),
+        "layernorm_fwd": (lambda: Nm.layernorm_fwd(x, w, b, cfg.eps, True), lfb),
+        "layernorm_bwd": (lambda: Nm.layernorm_bwd(dy, x, w, mean, lrstd, True, True, p_like=w), lbb),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(warmup):
+            fn()
+        ms = _events_time(fn, steps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": ms, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS, "bytes": nbytes}
+    return out
+
+
+def time_autograd_step(cfg, dtype, steps, warmup):
+    """User-facing path: autograd Function forward + backward (allocations included)."""
+    import numpy as np
+    import torch
+
+    from scree_amd.kernels.hip import varlen_attention_hip_autograd
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    n, h, d = cfg.total, cfg.heads, cfg.head_dim
+    q, k, v, do = (torch.randn(n, h, d, device=dev, dtype=dtype, generator=g) for _ in range(4))
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    off = np.zeros(len(cfg.lengths) + 1, dtype=np.int32)
+    off[1:] = np.cumsum(cfg.lengths)
+    cu = torch.from_numpy(off).to(dev)
+
+    def step():
+        out = varlen_attention_hip_autograd(q, k, v, cu, causal=cfg.causal)
+        out.backward(do)
+
+    for _ in range(warmup):
+        step()
+    ms = _events_time(step, steps)
+    return {"ms": ms, "tflops": cfg.fwd_flops() * 3.5 / (ms * 1e-3) / 1e12}
+
+
+def cpu_baseline(cfg, heads_sample=2, iters=3):
+    """The oracle (reference numpy einsum path, fp32, single-threaded) on a head sample."""
+    import numpy as np
+
+    from oracle.attention import attention_bwd, attention_fwd
+    from scree_amd import workloads
+
+    rng = np.random.default_rng(0)
+    n, d = cfg.total, cfg.head_dim
+    q, k, v, do = (rng.standard_normal((n, heads_sample, d)).astype(np.float32) for _ in range(4))
+    off = np.zeros(len(cfg.lengths) + 1, dtype=np.int32)
+    off[1:] = np.cumsum(cfg.lengths)
+
+    def run():
+        o, lse = attention_fwd(q, k, v, off, causal=cfg.causal, dtype=np.float32, impl="einsum")
+        attention_bwd(do, q, k, v, o, lse, off, causal=cfg.causal, dtype=np.float32, impl="einsum")
+
+    run()  # warmup
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    flops = 3.5 * workloads.attn_fwd_flops(cfg.lengths, heads_sample, d, cfg.causal)
+    return {
+        "value": flops / sec / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"config 4 forward+backward on {heads_sample} of {cfg.heads} heads (all "
+                   f"{len(cfg.lengths)} sequences, {n} tokens), fp32 numpy einsum as in the "
+                   f"reference's numpy branch; median of {iters} after 1 warmup; "
+                   f"{sec * 1e3:.0f} ms per sample step; host os.cpu_count()={os.cpu_count()}, "
+                   f"affinity={len(os.sched_getaffinity(0))}"),
+    }
+
+
+def load_traffic(kernel: str, workload: str):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    ent = data.get(workload, {}).get(kernel)
+    return None if ent is None else ent.get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--primary-only", action="store_true", help="skip the secondary configs")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the varlen "
+              "path has no multi-GPU mode. Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from scree_amd import workloads
+    from scree_amd.kernels.hip import _ffi
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    _ffi.lib()  # raise now if the library is missing
+    torch.cuda.set_device(0)
+    fp16 = torch.float16
+
+    cfg4 = workloads.config4()
+    log(f"primary: {cfg4.name} lengths={cfg4.lengths}")
+    prim, _ = time_attention(cfg4, fp16, args.steps, args.warmup, backward=True, per_kernel=True)
+    log(f"primary: {prim['ms']:.4f} ms/step, {prim['tflops']:.1f} TFLOP/s")
+
+    # roofline of the dominant kernel: algorithmic FLOPs it owns / its launch time
+    f_fwd = cfg4.fwd_flops()
+    owned = {"attn_schedule": 0.0, "attn_fwd": f_fwd, "attn_bwd_dq": 0.5 * f_fwd,
+             "attn_bwd_dkv": 2.0 * f_fwd}
+    kms = prim["kernels_ms"]
+    dom = max(kms, key=kms.get)
+    achieved = owned[dom] / (kms[dom] * 1e-3) / 1e12
+    roofline = {
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_F16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_F16_TFLOPS, 4),
+        "traffic": load_traffic(dom, "cfg4"),
+        "kernel": dom,
+        "avg_launch_us": round(kms[dom] * 1e3, 2),
+        "algorithmic_flops_per_launch": owned[dom],
+    }
+
+    secondary = {"cfg4_kernels_us": {k: round(v * 1e3, 2) for k, v in kms.items()}}
+    if not args.primary_only:
+        small = max(3, args.steps // 2)
+        cfg3 = workloads.config3()
+        r, _ = time_attention(cfg3, fp16, args.steps, args.warmup, backward=False, per_kernel=True)
+        secondary["cfg3_fwd"] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 2),
+                                 "mfma_frac": round(r["mfma_frac"], 4),
+                                 "kernels_us": {k: round(v * 1e3, 2) for k, v in r["kernels_ms"].items()}}
+        log(f"cfg3 fwd: {r['ms']:.4f} ms {r['tflops']:.1f} TFLOP/s")
+        for name, c, bwd in (("cfg3_fwd_fixed_h100_list", workloads.config3(fixed=True), False),
+                             ("cfg4_fwd_bwd_fixed_h100_list", workloads.config4(fixed=True), True)):
+            r, _ = time_attention(c, fp16, args.steps, args.warmup, backward=bwd)
+            secondary[name] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 2),
+                               "mfma_frac": round(r["mfma_frac"], 4)}
+            log(f"{name}: {r['ms']:.4f} ms {r['tflops']:.1f} TFLOP/s")
+        au = time_autograd_step(cfg4, fp16, args.steps, args.warmup)
+        secondary["cfg4_autograd_user_call"] = {"ms": round(au["ms"], 4), "tflops": round(au["tflops"], 2)}
+        cfg5 = workloads.config5()
+        r, _ = time_attention(cfg5, torch.bfloat16, small, 2, backward=True, per_kernel=True)
+        secondary["cfg5_fwd_bwd_bf16"] = {"ms": round(r["ms"], 3), "tflops": round(r["tflops"], 2),
+                                          "mfma_frac": round(r["mfma_frac"], 4),
+                                          "kernels_us": {k: round(v * 1e3, 1) for k, v in r["kernels_ms"].items()}}
+        log(f"cfg5: {r['ms']:.3f} ms {r['tflops']:.1f} TFLOP/s")
+        nr = time_norms(workloads.config2(), args.steps, args.warmup)
+        secondary["cfg2_norms_bf16"] = {k: {"us": round(v["ms"] * 1e3, 2), "GB/s": round(v["GB/s"], 1),
+                                            "hbm_frac": round(v["hbm_frac"], 4)} for k, v in nr.items()}
+        log("cfg2: " + ", ".join(f"{k} {v['GB/s']:.0f} GB/s" for k, v in nr.items()))
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(cfg4)
+        log(f"cpu: {cpu['value'] * 1e3:.3f} GFLOP/s")
+
+    line = {
+        "metric": "causal varlen attn fwd & fwd+bwd TFLOP/s, MFMA %; varlen RMSNorm HBM GB/s",
+        "value": round(prim["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(prim["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1), resident in HBM",
+        "config": {
+            "workload": ("cfg4: causal varlen attention forward+backward (scheduler + fwd + dQ + dK/dV), "
+                         f"fp16, {len(cfg4.lengths)} seqs, {cfg4.total} tokens (log-normal sigma 0.6 "
+                         f"rescaled), {cfg4.heads} heads x head_dim {cfg4.head_dim}"),
+            "lengths": cfg4.lengths,
+            "mfma_frac": round(prim["mfma_frac"], 4),
+            "parallelism": "single GPU",
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -102,6 +102,25 @@ int scree_attn_bwd(const void* dout, const void* q, const void* k, const void* v
                    int head_dim, const int64_t* strides, float softmax_scale, int causal,
                    int dtype, const void* workspace, size_t workspace_bytes, void* stream);
 
+/* The two stages of scree_attn_bwd, for callers that schedule or time them
+ * separately; dq must run first because it writes delta.
+ * scree_attn_bwd_dq: dq and delta.  strides[12] = {dout, q, k, v, o, dq} x {row, head}.
+ * scree_attn_bwd_dkv: dk and dv from delta.  strides[12] = {dout, q, k, v, dk, dv} x {row, head}.
+ * Together they replace the reference's three backward kernels
+ * (src/scree/kernels/triton/_backward.py:36-285): Delta is folded into the
+ * dQ pass. */
+int scree_attn_bwd_dq(const void* dout, const void* q, const void* k, const void* v,
+                      const void* o, const float* lse, void* dq, float* delta,
+                      const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                      int head_dim, const int64_t* strides, float softmax_scale, int causal,
+                      int dtype, const void* workspace, size_t workspace_bytes, void* stream);
+
+int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k, const void* v,
+                       const float* lse, const float* delta, void* dk, void* dv,
+                       const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                       int head_dim, const int64_t* strides, float softmax_scale, int causal,
+                       int dtype, const void* workspace, size_t workspace_bytes, void* stream);
+
 /* -------------------------------------------------------------------- norms
  * Replace varlen_rmsnorm_triton (src/scree/kernels/triton/varlen_rmsnorm.py:17-99)
  * and varlen_layernorm_triton (src/scree/kernels/triton/varlen_layernorm.py:14-109).

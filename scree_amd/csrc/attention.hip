@@ -203,81 +203,89 @@ __global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __re
 }
 
 // ------------------------------------------------------- tile staging
-// Copies ROWS rows x D columns of a (tokens, heads, D) tensor, rows
-// [row0, row0 + ROWS) of one head, through registers into LDS.  Rows at or
-// past `limit` are zero-filled, so masked work never reads stale data.
+// Raw buffer resource for `bytes` bytes at `base` (gfx9 descriptor: stride 0,
+// dword3 = 0x00020000).  Loads at offsets past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+}
+
+// A ROWS x D tile of one head, staged row-major through registers into LDS.
+// Loads go through a buffer descriptor that covers only the rows below
+// `limit`, so rows past the sequence end read as zeros and nothing outside
+// it is touched; the per-thread byte offsets are fixed and computed once.
 template <typename T, int D, int ROWS>
 struct Stage {
-  static constexpr int CPR = D / 8;                       // 16-byte chunks per row
-  static constexpr int TOTAL = ROWS * CPR;
-  static constexpr int CH = (TOTAL + kThreads - 1) / kThreads;
+  static constexpr int CPR = D / 8;  // 16-byte chunks per row
+  static constexpr int UNITS = ROWS * CPR;
+  static_assert(UNITS % kThreads == 0, "tile must split evenly over the block");
+  static constexpr int CH = UNITS / kThreads;
+  uint32_t off[CH];
   uint4 r[CH];
 
-  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t row_stride, int row0,
-                                       int limit) {
+  __device__ __forceinline__ void init(int64_t row_stride) {
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const int c = j * kThreads + threadIdx.x;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      r[j] = make_uint4(0, 0, 0, 0);
-      if (c < TOTAL && row0 + row < limit) r[j] = ld16(base + (int64_t)(row0 + row) * row_stride + col);
+      const int u = j * kThreads + threadIdx.x;
+      off[j] = (uint32_t)(((int64_t)(u / CPR) * row_stride + (u % CPR) * 8) * (int64_t)sizeof(T));
     }
+  }
+  // rows [row0, row0 + ROWS) of a sequence starting at `base`; rows >= limit read as 0
+  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t row_stride, int row0,
+                                       int limit) {
+    const int valid = min(ROWS, limit - row0);
+    const uint32_t bytes = valid > 0 ? (uint32_t)((int64_t)valid * row_stride * (int64_t)sizeof(T)) : 0u;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)row0 * row_stride, bytes);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) r[j] = buf_ld16(rs, off[j]);
   }
   // lds[row][col], leading dimension ld (elements)
   __device__ __forceinline__ void put_rows(T* lds, int ld) const {
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const int c = j * kThreads + threadIdx.x;
-      if (c < TOTAL) {
-        const int row = c / CPR, col = (c % CPR) * 8;
-        st16(lds + row * ld + col, r[j]);
-      }
-    }
-  }
-  // lds[col][row] (transposed), leading dimension ld (elements)
-  __device__ __forceinline__ void put_cols(T* lds, int ld) const {
-    uint16_t* l16 = reinterpret_cast<uint16_t*>(lds);
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int c = j * kThreads + threadIdx.x;
-      if (c < TOTAL) {
-        const int row = c / CPR, col = (c % CPR) * 8;
-        const uint32_t w[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          l16[(col + e) * ld + row] = (uint16_t)((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-      }
+      const int u = j * kThreads + threadIdx.x;
+      st16(lds + (u / CPR) * ld + (u % CPR) * 8, r[j]);
     }
   }
 };
 
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 lds_frag16(const T* p) {
-  return *reinterpret_cast<const typename VecT<T>::x8*>(p);
+  return __builtin_bit_cast(typename VecT<T>::x8, *reinterpret_cast<const uint4*>(p));
 }
-// Two 4-element runs (p[0..3], p[8..11]) as one 8-element operand.
+// Transposed operand from a row-major LDS tile X[row][col] (leading dim ld).
+// ds_read_tr16_b64 hands lane 16G + i, slot j, element i%4 of the 8 bytes
+// addressed by lane 16G + 4j + i/4.  With each lane addressing
+// X[4g + (lr%16)/4][16*(lr/16) + 4*(lr%4)] (tr_lane_offset), lane (lr, g)
+// receives X[4g + j][lr] in slots j = 0..3; a second read 8 rows further
+// gives slots 4..7.  That is the k-run layout {4g + 0..3, 8 + 4g + 0..3} of
+// the MFMA operands here (rows of X are the k axis, columns the M axis).
+__device__ __forceinline__ int tr_lane_offset(int lr, int g, int ld) {
+  return (4 * g + ((lr & 15) >> 2)) * ld + 16 * (lr >> 4) + 4 * (lr & 3);
+}
 template <typename T>
-__device__ __forceinline__ typename VecT<T>::x8 lds_frag_2x4(const T* p) {
-  typedef typename VecT<T>::x4 x4;
-  typedef typename VecT<T>::x8 x8;
-  const x4 a = *reinterpret_cast<const x4*>(p);
-  const x4 b = *reinterpret_cast<const x4*>(p + 8);
-  x8 out;
-  out[0] = a[0]; out[1] = a[1]; out[2] = a[2]; out[3] = a[3];
-  out[4] = b[0]; out[5] = b[1]; out[6] = b[2]; out[7] = b[3];
-  return out;
+__device__ __forceinline__ typename VecT<T>::x8 lds_frag_tr(const T* p, int ld) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  typedef __attribute__((address_space(3))) s4* lds_s4;
+  const s4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p));
+  const s4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p + 8 * ld));
+  const s8 v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  return __builtin_bit_cast(typename VecT<T>::x8, v);
 }
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 gmem_frag16(const T* p) {
-  return *reinterpret_cast<const typename VecT<T>::x8*>(p);
+  return __builtin_bit_cast(typename VecT<T>::x8, ld16(p));
 }
-// Elements e0..e0+7 of a 16-float accumulator, rounded, as an operand.
+// Elements e0..e0+7 of a 16-float accumulator, rounded to T, as an operand.
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 pack_frag(const f32x16& c, int e0) {
-  typename VecT<T>::x8 out;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) out[j] = (T)c[e0 + j];
-  return out;
+  const uint4 u = make_uint4(pack2<T>(c[e0 + 0], c[e0 + 1]), pack2<T>(c[e0 + 2], c[e0 + 3]),
+                             pack2<T>(c[e0 + 4], c[e0 + 5]), pack2<T>(c[e0 + 6], c[e0 + 7]));
+  return __builtin_bit_cast(typename VecT<T>::x8, u);
 }
 // Store the 16 values of one 32x32 accumulator column-slice: element i is
 // D-index d0 + 8*(i/4) + 4g + i%4 of a row; scaled by `mul`.
@@ -303,32 +311,47 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-// Row index (within a 32-row MFMA tile) held in accumulator element i.
-__device__ __forceinline__ int acc_row(int i, int g) { return 8 * (i >> 2) + 4 * g + (i & 3); }
+// Row (within a 32-row MFMA tile, lane group g = 0) of accumulator element i;
+// lane group g adds 4g.
+constexpr int acc_row0(int i) { return 8 * (i >> 2) + (i & 3); }
+
+// Mask (to -inf) the elements of a 32x32 tile whose row exceeds `rel`:
+// element i is row acc_row0(i) + 4g, so the test is acc_row0(i) > rel - 4g.
+__device__ __forceinline__ void mask_rows_above(f32x16& c, int rel_minus_4g) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (acc_row0(i) > rel_minus_4g) c[i] = kNegInf;
+}
+
+// Wave index as a scalar, so per-wave tile bounds are uniform branches.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
 
 struct Strides {
   int64_t row, head;
 };
 
+// A softmax row's reference maximum is raised only when the block maximum
+// exceeds it by more than this many powers of two; p = 2^(s*c - m*c) then
+// stays <= 2^8, which fp32 sums and fp16/bf16 operands hold exactly as well
+// as values <= 1 (same relative precision), and most blocks skip the O rescale.
+constexpr float kRescaleLog2Gap = 8.0f;
+
 // ---------------------------------------------------------------- forward
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
-    float* __restrict__ lse, const int32_t* __restrict__ cu, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int heads, Strides sq, Strides sk, Strides sv, Strides so,
-    float scale, float scale_log2) {
-  constexpr int KLD = D + 8;    // sK leading dim (16-byte pad)
-  constexpr int VLD = kBN + 4;  // sVt leading dim (8-byte pad)
-  __shared__ __align__(16) T sK[kBN * KLD];
-  __shared__ __align__(16) T sVt[D * VLD];
+    float* __restrict__ lse, const int32_t* __restrict__ header, const int4* __restrict__ items,
+    int heads, Strides sq, Strides sk, Strides sv, Strides so, float scale, float scale_log2) {
+  constexpr int KLD = D + 8;    // sK leading dim: 16-byte pad, row reads conflict-free
+  constexpr int VLD = D + 16;   // sV leading dim: 32-byte pad, transposed reads conflict-free
+  constexpr int BUF = kBN * KLD + kBN * VLD;
+  __shared__ __align__(16) T smem[2 * BUF];
 
   const int item = blockIdx.x / heads, h = blockIdx.x % heads;
   if (item >= header[0]) return;
   const int4 it = items[item];
-  const int start = it.z;
-  const int L = it.w;
-  const int q0 = it.y * kBM;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int start = it.z, L = it.w, q0 = it.y * kBM;
+  const int wave = wave_id(), lane = threadIdx.x & (kWave - 1);
   const int g = lane >> 5, lr = lane & 31;
   const int qw0 = q0 + 32 * wave;
   const int my_q = qw0 + lr;
@@ -339,21 +362,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
 
   typedef typename VecT<T>::x8 x8;
   x8 qf[D / 16];
-  {
-    const T* qrow = q + (int64_t)(start + my_q) * sq.row + (int64_t)h * sq.head;
+  {  // rows past L read row L-1: their results are never stored
+    const T* qrow = q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      if (my_q < L) qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
-      else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) qf[s][j] = (T)0.f;
-      }
-    }
+    for (int s = 0; s < D / 16; ++s) qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
   }
 
   const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
   const int nkb = (kend_wg + kBN - 1) / kBN;
   const int kend_wave = wave_live ? (CAUSAL ? min(L, qw0 + 32) : L) : 0;
+  const float rescale_gap = kRescaleLog2Gap / scale_log2;
 
   f32x16 oacc[D / 32];
 #pragma unroll
@@ -361,86 +379,97 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   float m_run = kNegInf, l_run = 0.f;
 
   Stage<T, D, kBN> stK, stV;
+  stK.init(sk.row);
+  stV.init(sv.row);
   stK.load(kh, sk.row, 0, L);
   stV.load(vh, sv.row, 0, L);
+  stK.put_rows(smem, KLD);
+  stV.put_rows(smem + kBN * KLD, VLD);
+  __syncthreads();
+  const int vtr = tr_lane_offset(lr, g, VLD);
 
   for (int kb = 0; kb < nkb; ++kb) {
-    __syncthreads();
-    stK.put_rows(sK, KLD);
-    stV.put_cols(sVt, VLD);
-    __syncthreads();
+    const T* sK = smem + (kb & 1) * BUF;
+    const T* sV = sK + kBN * KLD;
     if (kb + 1 < nkb) {
       stK.load(kh, sk.row, (kb + 1) * kBN, L);
       stV.load(vh, sv.row, (kb + 1) * kBN, L);
     }
     const int kbase = kb * kBN;
     const int nt = kbase < kend_wave ? (kbase + 32 < kend_wave ? 2 : 1) : 0;
-    if (nt == 0) continue;
-
-    f32x16 sacc[2];
+    if (nt > 0) {
+      f32x16 sacc[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (t < nt) {
-        sacc[t] = zero16();
+      for (int t = 0; t < 2; ++t) {
+        if (t < nt) {
+          sacc[t] = zero16();
 #pragma unroll
-        for (int s = 0; s < D / 16; ++s)
-          sacc[t] = mfma32(lds_frag16(sK + (32 * t + lr) * KLD + 16 * s + 8 * g), qf[s], sacc[t]);
+          for (int s = 0; s < D / 16; ++s)
+            sacc[t] = mfma32(lds_frag16(sK + (32 * t + lr) * KLD + 16 * s + 8 * g), qf[s], sacc[t]);
+        }
       }
-    }
-    const bool need_mask = (kbase + 32 * nt > L) || (CAUSAL && kbase + 32 * nt - 1 > qw0);
-    if (need_mask) {
+      if (CAUSAL) {
+        // only the tile starting at qw0 straddles the diagonal: keys > my_q
+        if (kbase + 32 * (nt - 1) == qw0) {
+          if (nt == 1) mask_rows_above(sacc[0], lr - 4 * g);
+          else mask_rows_above(sacc[1], lr - 4 * g);
+        }
+      } else if (kbase + 32 * nt > L) {
+        // keys >= L hold zeros; drop them from the softmax
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          if (t < nt) mask_rows_above(sacc[t], L - 1 - (kbase + 32 * t) - 4 * g);
+      }
+      float mx = kNegInf;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        if (t < nt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[t][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const bool grow = mx > m_run + rescale_gap;
+      if (__any(grow)) {
+        const float m_new = grow ? mx : m_run;
+        const float alpha = fast_exp2((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+        m_run = m_new;
+      }
+      const float mb = m_run == kNegInf ? 0.f : m_run * scale_log2;
+      float psum = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        if (t < nt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float p = fast_exp2(fmaf(sacc[t][i], scale_log2, -mb));
+            sacc[t][i] = p;
+            psum += p;
+          }
+      l_run += psum;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if (t < nt) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int kk = kbase + 32 * t + acc_row(i, g);
-            const bool ok = kk < L && (!CAUSAL || kk <= my_q);
-            if (!ok) sacc[t][i] = kNegInf;
+          for (int hh = 0; hh < 2; ++hh) {
+            const x8 pf = pack_frag<T>(sacc[t], 8 * hh);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+              oacc[dt] = mfma32(lds_frag_tr(sV + vtr + (32 * t + 16 * hh) * VLD + 32 * dt, VLD), pf,
+                                oacc[dt]);
           }
         }
       }
     }
-    float mx = kNegInf;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      if (t < nt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[t][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = fast_exp2((m_run - m_use) * scale_log2);
-    const float mb = m_use * scale_log2;
-    float psum = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      if (t < nt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float p = fast_exp2(sacc[t][i] * scale_log2 - mb);
-          sacc[t][i] = p;
-          psum += p;
-        }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (t < nt) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const x8 pf = pack_frag<T>(sacc[t], 8 * hh);
-#pragma unroll
-          for (int dt = 0; dt < D / 32; ++dt)
-            oacc[dt] = mfma32(lds_frag_2x4(sVt + (32 * dt + lr) * VLD + 32 * t + 16 * hh + 4 * g), pf,
-                              oacc[dt]);
-        }
-      }
+    if (kb + 1 < nkb) {
+      T* nK = smem + ((kb + 1) & 1) * BUF;
+      stK.put_rows(nK, KLD);
+      stV.put_rows(nK + kBN * KLD, VLD);
     }
+    __syncthreads();
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
@@ -457,29 +486,32 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
 // Per item: 128 queries (32 per wave) loop over 64-key blocks.
 //   S^T = K Q^T, dP^T = V dO^T (Q, dO operands in registers; K, V from LDS)
 //   P^T = exp(S^T - LSE), dS^T = P^T (dP^T - Delta)
-//   dQ^T += K^T dS^T (K^T from LDS, dS^T from registers)
+//   dQ^T += K^T dS^T (K^T read transposed from the row-major K tile; dS^T in registers)
 // Delta = rowsum(O * dO) is computed here from the stored O and written out
-// for the dK/dV pass.
+// for the dK/dV pass.  Keys past L hold zeros in K and V, so their dS^T
+// multiplies a zero row of K^T: no length mask is needed.
+template <typename T, int D>
+constexpr int dq_buffers() {
+  return 2;
+}
+
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
-    float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ cu,
-    const int32_t* __restrict__ header, const int4* __restrict__ items, int heads, Strides sdo,
-    Strides sq, Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2) {
+    float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ header,
+    const int4* __restrict__ items, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
+    Strides so, Strides sdq, float scale, float scale_log2) {
+  constexpr int NBUF = dq_buffers<T, D>();
   constexpr int KLD = D + 8;
-  constexpr int KTLD = kBN + 4;
-  __shared__ __align__(16) T sK[kBN * KLD];
-  __shared__ __align__(16) T sKt[D * KTLD];
-  __shared__ __align__(16) T sV[kBN * KLD];
+  constexpr int BUF = 2 * kBN * KLD;  // K rows, V rows
+  __shared__ __align__(16) T smem[NBUF * BUF];
 
   const int item = blockIdx.x / heads, h = blockIdx.x % heads;
   if (item >= header[0]) return;
   const int4 it = items[item];
-  const int start = it.z;
-  const int L = it.w;
-  const int q0 = it.y * kBM;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int start = it.z, L = it.w, q0 = it.y * kBM;
+  const int wave = wave_id(), lane = threadIdx.x & (kWave - 1);
   const int g = lane >> 5, lr = lane & 31;
   const int qw0 = q0 + 32 * wave;
   const int my_q = qw0 + lr;
@@ -490,29 +522,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   x8 qf[D / 16], df[D / 16];
   float dl = 0.f;
   {
-    const int64_t tok = start + my_q;
+    const int64_t tok = start + min(my_q, L - 1);
     const T* qrow = q + tok * sq.row + (int64_t)h * sq.head;
     const T* drow = dout + tok * sdo.row + (int64_t)h * sdo.head;
     const T* orow = o + tok * so.row + (int64_t)h * so.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
-      if (row_ok) {
-        qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
-        df[s] = gmem_frag16(drow + 16 * s + 8 * g);
-        const x8 of = gmem_frag16(orow + 16 * s + 8 * g);
+      qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
+      df[s] = gmem_frag16(drow + 16 * s + 8 * g);
+      const x8 of = gmem_frag16(orow + 16 * s + 8 * g);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)df[s][j];
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          qf[s][j] = (T)0.f;
-          df[s][j] = (T)0.f;
-        }
-      }
+      for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)df[s][j];
     }
   }
   dl += __shfl_xor(dl, 32, kWave);
-  const float lse2 = row_ok ? lse[(int64_t)(start + my_q) * heads + h] * kLog2e : 0.f;
+  const float lse2 = lse[(int64_t)(start + min(my_q, L - 1)) * heads + h] * kLog2e;
   if (row_ok && g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
 
   const T* kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
@@ -526,22 +550,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   for (int dt = 0; dt < D / 32; ++dt) dqacc[dt] = zero16();
 
   Stage<T, D, kBN> stK, stV;
+  stK.init(sk.row);
+  stV.init(sv.row);
   stK.load(kh, sk.row, 0, L);
   stV.load(vh, sv.row, 0, L);
+  stK.put_rows(smem, KLD);
+  stV.put_rows(smem + kBN * KLD, KLD);
+  __syncthreads();
+  const int ktr = tr_lane_offset(lr, g, KLD);
   for (int kb = 0; kb < nkb; ++kb) {
-    __syncthreads();
-    stK.put_rows(sK, KLD);
-    stK.put_cols(sKt, KTLD);
-    stV.put_rows(sV, KLD);
-    __syncthreads();
+    const T* sK = smem + (NBUF == 2 ? (kb & 1) : 0) * BUF;
+    const T* sV = sK + kBN * KLD;
     if (kb + 1 < nkb) {
       stK.load(kh, sk.row, (kb + 1) * kBN, L);
       stV.load(vh, sv.row, (kb + 1) * kBN, L);
     }
     const int kbase = kb * kBN;
     const int nt = kbase < kend_wave ? (kbase + 32 < kend_wave ? 2 : 1) : 0;
-    if (nt == 0) continue;
-    const bool need_mask = (kbase + 32 * nt > L) || (CAUSAL && kbase + 32 * nt - 1 > qw0);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (t >= nt) continue;
@@ -551,14 +576,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
         sacc = mfma32(lds_frag16(sK + (32 * t + lr) * KLD + 16 * s + 8 * g), qf[s], sacc);
         pacc = mfma32(lds_frag16(sV + (32 * t + lr) * KLD + 16 * s + 8 * g), df[s], pacc);
       }
+      if (CAUSAL && kbase + 32 * t == qw0) mask_rows_above(sacc, lr - 4 * g);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float p = fast_exp2(sacc[i] * scale_log2 - lse2);
-        if (need_mask) {
-          const int kk = kbase + 32 * t + acc_row(i, g);
-          const bool ok = kk < L && (!CAUSAL || kk <= my_q);
-          if (!ok) p = 0.f;
-        }
+        const float p = fast_exp2(fmaf(sacc[i], scale_log2, -lse2));
         sacc[i] = p * (pacc[i] - dl);  // dS^T
       }
 #pragma unroll
@@ -566,10 +587,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
         const x8 sf = pack_frag<T>(sacc, 8 * hh);
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
-          dqacc[dt] = mfma32(lds_frag_2x4(sKt + (32 * dt + lr) * KTLD + 32 * t + 16 * hh + 4 * g), sf,
+          dqacc[dt] = mfma32(lds_frag_tr(sK + ktr + (32 * t + 16 * hh) * KLD + 32 * dt, KLD), sf,
                              dqacc[dt]);
       }
     }
+    if (kb + 1 < nkb) {
+      if (NBUF == 1) __syncthreads();
+      T* nK = smem + (NBUF == 2 ? ((kb + 1) & 1) : 0) * BUF;
+      stK.put_rows(nK, KLD);
+      stV.put_rows(nK + kBN * KLD, KLD);
+    }
+    __syncthreads();
   }
   if (wave_live && row_ok) {
     T* out = dq + (int64_t)(start + my_q) * sdq.row + (int64_t)h * sdq.head;
@@ -582,35 +610,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
 // Per item: 128 keys (32 per wave) loop over blocks of BQ queries.
 //   S = Q K^T, dP = dO V^T (K, V operands in registers; Q, dO from LDS)
 //   P = exp(S - LSE), dS = P (dP - Delta)
-//   dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T from LDS; P, dS in registers)
-// D = 128 holds K, V, dK and dV for 32 keys per lane group in registers and
-// needs the full register file (one wave per SIMD); smaller D fits two.
+//   dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T read transposed from the row-major
+//   LDS tiles; P, dS in registers)
+// Queries past L hold zeros in Q and dO (and LSE = Delta = 0), so they add
+// nothing to dK or dV: no length mask is needed.
+// D = 128 holds K, V, dK and dV for its keys in registers and needs the full
+// register file (one wave per SIMD); smaller D fits two.
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
-    T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ cu,
-    const int32_t* __restrict__ header, const int4* __restrict__ items, int heads, Strides sdo,
-    Strides sq, Strides sk, Strides sv, Strides sdk, Strides sdv, float scale, float scale_log2) {
+    T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ header,
+    const int4* __restrict__ items, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
+    Strides sdk, Strides sdv, float scale, float scale_log2) {
   constexpr int BQ = D >= 128 ? 32 : 64;
   constexpr int NQT = BQ / 32;
   constexpr int LD = D + 8;
-  constexpr int TLD = BQ + 4;
-  __shared__ __align__(16) T sQ[BQ * LD];
-  __shared__ __align__(16) T sQt[D * TLD];
-  __shared__ __align__(16) T sO[BQ * LD];   // dO rows
-  __shared__ __align__(16) T sOt[D * TLD];  // dO transposed
-  __shared__ __align__(16) float sL[BQ];
-  __shared__ __align__(16) float sDl[BQ];
+  constexpr int BUF = 2 * BQ * LD;  // Q rows, dO rows
+  __shared__ __align__(16) T smem[2 * BUF];
+  __shared__ __align__(16) float sLD[2][2][BQ];  // [buffer][lse*log2e | delta][row]
 
   const int item = blockIdx.x / heads, h = blockIdx.x % heads;
   if (item >= header[0]) return;
   const int4 it = items[item];
-  const int start = it.z;
-  const int L = it.w;
+  const int start = it.z, L = it.w;
   const int nblk = (L + kBM - 1) / kBM;
   const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int wave = wave_id(), lane = threadIdx.x & (kWave - 1);
   const int g = lane >> 5, lr = lane & 31;
   const int kw0 = k0 + 32 * wave;
   const int my_k = kw0 + lr;
@@ -620,20 +646,13 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
   typedef typename VecT<T>::x8 x8;
   x8 kf[D / 16], vf[D / 16];
   {
-    const T* krow = k + (int64_t)(start + my_k) * sk.row + (int64_t)h * sk.head;
-    const T* vrow = v + (int64_t)(start + my_k) * sv.row + (int64_t)h * sv.head;
+    const int64_t tok = start + min(my_k, L - 1);
+    const T* krow = k + tok * sk.row + (int64_t)h * sk.head;
+    const T* vrow = v + tok * sv.row + (int64_t)h * sv.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
-      if (key_ok) {
-        kf[s] = gmem_frag16(krow + 16 * s + 8 * g);
-        vf[s] = gmem_frag16(vrow + 16 * s + 8 * g);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          kf[s][j] = (T)0.f;
-          vf[s][j] = (T)0.f;
-        }
-      }
+      kf[s] = gmem_frag16(krow + 16 * s + 8 * g);
+      vf[s] = gmem_frag16(vrow + 16 * s + 8 * g);
     }
   }
   f32x16 dkacc[D / 32], dvacc[D / 32];
@@ -649,81 +668,96 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
   const int nqb = L > qbeg ? (L - qbeg + BQ - 1) / BQ : 0;
 
   Stage<T, D, BQ> stQ, stO;
+  stQ.init(sq.row);
+  stO.init(sdo.row);
   float pl = 0.f, pd = 0.f;
   auto load_block = [&](int qb) {
     stQ.load(qh, sq.row, qb, L);
     stO.load(dh, sdo.row, qb, L);
     if (threadIdx.x < BQ) {
       const int qq = qb + threadIdx.x;
-      pl = qq < L ? lse[(int64_t)(start + qq) * heads + h] * kLog2e : 0.f;
-      pd = qq < L ? delta[(int64_t)(start + qq) * heads + h] : 0.f;
+      const int64_t idx = (int64_t)(start + min(qq, L - 1)) * heads + h;
+      pl = qq < L ? lse[idx] * kLog2e : 0.f;
+      pd = qq < L ? delta[idx] : 0.f;
     }
   };
-  if (nqb > 0) load_block(qbeg);
+  auto put_block = [&](int buf) {
+    T* b = smem + buf * BUF;
+    stQ.put_rows(b, LD);
+    stO.put_rows(b + BQ * LD, LD);
+    if (threadIdx.x < BQ) {
+      sLD[buf][0][threadIdx.x] = pl;
+      sLD[buf][1][threadIdx.x] = pd;
+    }
+  };
+  if (nqb > 0) {
+    load_block(qbeg);
+    put_block(0);
+  }
+  __syncthreads();
+  const int qtr = tr_lane_offset(lr, g, LD);
   for (int b = 0; b < nqb; ++b) {
     const int qb = qbeg + b * BQ;
-    __syncthreads();
-    stQ.put_rows(sQ, LD);
-    stQ.put_cols(sQt, TLD);
-    stO.put_rows(sO, LD);
-    stO.put_cols(sOt, TLD);
-    if (threadIdx.x < BQ) {
-      sL[threadIdx.x] = pl;
-      sDl[threadIdx.x] = pd;
-    }
-    __syncthreads();
+    const T* sQ = smem + (b & 1) * BUF;
+    const T* sO = sQ + BQ * LD;
+    const float* sL = sLD[b & 1][0];
+    const float* sDl = sLD[b & 1][1];
     if (b + 1 < nqb) load_block(qb + BQ);
-    if (!wave_live) continue;
+    if (wave_live) {
 #pragma unroll
-    for (int u = 0; u < NQT; ++u) {
-      const int qt0 = qb + 32 * u;
-      if (qt0 >= L) continue;
-      if (CAUSAL && qt0 + 31 < kw0) continue;  // every query of the tile precedes every key
-      f32x16 sacc = zero16(), pacc = zero16();
+      for (int u = 0; u < NQT; ++u) {
+        const int qt0 = qb + 32 * u;
+        if (qt0 >= L) continue;
+        if (CAUSAL && qt0 < kw0) continue;  // every query of the tile precedes every key
+        f32x16 sacc = zero16(), pacc = zero16();
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
-        sacc = mfma32(lds_frag16(sQ + (32 * u + lr) * LD + 16 * s + 8 * g), kf[s], sacc);
-        pacc = mfma32(lds_frag16(sO + (32 * u + lr) * LD + 16 * s + 8 * g), vf[s], pacc);
-      }
-      // lane: key my_k (column), queries qt0 + acc_row(i, g) (rows)
-      const bool need_mask = (qt0 + 32 > L) || (CAUSAL && qt0 < kw0 + 31);
-      float pv[16];
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int r0 = 32 * u + 8 * i4 + 4 * g;
-        const float4 l4 = *reinterpret_cast<const float4*>(sL + r0);
-        const float4 d4 = *reinterpret_cast<const float4*>(sDl + r0);
-        const float la[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float da[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * i4 + e;
-          float p = fast_exp2(sacc[i] * scale_log2 - la[e]);
-          if (need_mask) {
-            const int qq = qt0 + acc_row(i, g);
-            const bool ok = qq < L && (!CAUSAL || qq >= my_k);
-            if (!ok) p = 0.f;
-          }
-          pv[i] = p;
-          sacc[i] = p * (pacc[i] - da[e]);  // dS
+        for (int s = 0; s < D / 16; ++s) {
+          sacc = mfma32(lds_frag16(sQ + (32 * u + lr) * LD + 16 * s + 8 * g), kf[s], sacc);
+          pacc = mfma32(lds_frag16(sO + (32 * u + lr) * LD + 16 * s + 8 * g), vf[s], pacc);
         }
-      }
-      f32x16 pacc2;
+        // lane: key my_k (column); element i: query qt0 + acc_row0(i) + 4g (row)
+        f32x16 pv;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) pacc2[i] = pv[i];
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int r0 = 32 * u + 8 * i4 + 4 * g;
+          const float4 l4 = *reinterpret_cast<const float4*>(sL + r0);
+          const float4 d4 = *reinterpret_cast<const float4*>(sDl + r0);
+          const float la[4] = {l4.x, l4.y, l4.z, l4.w};
+          const float da[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const x8 pf = pack_frag<T>(pacc2, 8 * hh);
-        const x8 sf = pack_frag<T>(sacc, 8 * hh);
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * i4 + e;
+            const float p = fast_exp2(fmaf(sacc[i], scale_log2, -la[e]));
+            pv[i] = p;
+            sacc[i] = p * (pacc[i] - da[e]);  // dS
+          }
+        }
+        if (CAUSAL && qt0 == kw0) {
+          // diagonal tile: queries before the key contribute nothing
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          dvacc[dt] = mfma32(lds_frag_2x4(sOt + (32 * dt + lr) * TLD + 32 * u + 16 * hh + 4 * g), pf,
-                             dvacc[dt]);
-          dkacc[dt] = mfma32(lds_frag_2x4(sQt + (32 * dt + lr) * TLD + 32 * u + 16 * hh + 4 * g), sf,
-                             dkacc[dt]);
+          for (int i = 0; i < 16; ++i) {
+            if (acc_row0(i) < lr - 4 * g) {
+              pv[i] = 0.f;
+              sacc[i] = 0.f;
+            }
+          }
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const x8 pf = pack_frag<T>(pv, 8 * hh);
+          const x8 sf = pack_frag<T>(sacc, 8 * hh);
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt) {
+            dvacc[dt] = mfma32(lds_frag_tr(sO + qtr + (32 * u + 16 * hh) * LD + 32 * dt, LD), pf,
+                               dvacc[dt]);
+            dkacc[dt] = mfma32(lds_frag_tr(sQ + qtr + (32 * u + 16 * hh) * LD + 32 * dt, LD), sf,
+                               dkacc[dt]);
+          }
         }
       }
     }
+    if (b + 1 < nqb) put_block((b + 1) & 1);
+    __syncthreads();
   }
   if (wave_live && key_ok) {
     T* krow = dk + (int64_t)(start + my_k) * sdk.row + (int64_t)h * sdk.head;
@@ -747,6 +781,8 @@ int check_tensor(const char* fn, const char* name, const void* p, const int64_t*
     return set_error(SCREE_ERR_INVALID,
                      "%s: %s strides (%lld, %lld) must be non-negative multiples of 8 elements",
                      fn, name, (long long)st[0], (long long)st[1]);
+  if (st[0] >= ((int64_t)1 << 24) || st[1] >= ((int64_t)1 << 24))
+    return set_error(SCREE_ERR_INVALID, "%s: %s strides must be below 2^24 elements", fn, name);
   if (total > 1 && st[0] < head_dim)
     return set_error(SCREE_ERR_INVALID, "%s: %s row stride %lld overlaps rows", fn, name,
                      (long long)st[0]);
@@ -787,30 +823,43 @@ void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* l
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(o), lse, cu, header, items, heads, Strides{st[0], st[1]},
+                     static_cast<T*>(o), lse, header, items, heads, Strides{st[0], st[1]},
                      Strides{st[2], st[3]}, Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale,
                      scale * kLog2e);
 }
 
+// strides: {dout, q, k, v, o, dq} x {row, head}
 template <typename T, int D, bool C>
-void launch_bwd_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
-                  const float* lse, void* dq, void* dk, void* dv, float* delta, const int32_t* cu,
-                  int heads, const int64_t* st, float scale, int64_t grid, const void* ws,
-                  hipStream_t stream) {
+void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
+                     const float* lse, void* dq, float* delta, const int32_t* cu, int heads,
+                     const int64_t* st, float scale, int64_t grid, const void* ws,
+                     hipStream_t stream) {
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
-  const Strides sdo{st[0], st[1]}, sq{st[2], st[3]}, sk{st[4], st[5]}, sv{st[6], st[7]},
-      so{st[8], st[9]}, sdq{st[10], st[11]}, sdk{st[12], st[13]}, sdv{st[14], st[15]};
   hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<const T*>(o), lse, delta, static_cast<T*>(dq), cu, header, items,
-                     heads, sdo, sq, sk, sv, so, sdq, scale, scale * kLog2e);
+                     static_cast<const T*>(o), lse, delta, static_cast<T*>(dq), header, items,
+                     heads, Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
+                     Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
+                     scale * kLog2e);
+}
+
+// strides: {dout, q, k, v, dk, dv} x {row, head}
+template <typename T, int D, bool C>
+void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
+                      const float* lse, const float* delta, void* dk, void* dv, const int32_t* cu,
+                      int heads, const int64_t* st, float scale, int64_t grid, const void* ws,
+                      hipStream_t stream) {
+  const int32_t* header = static_cast<const int32_t*>(ws);
+  const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
   hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0,
                      stream, static_cast<const T*>(dout), static_cast<const T*>(q),
-                     static_cast<const T*>(k), static_cast<const T*>(v), lse,
-                     static_cast<const float*>(delta), static_cast<T*>(dk), static_cast<T*>(dv),
-                     cu, header, items, heads, sdo, sq, sk, sv, sdk, sdv, scale, scale * kLog2e);
+                     static_cast<const T*>(k), static_cast<const T*>(v), lse, delta,
+                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, heads,
+                     Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
+                     Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
+                     scale * kLog2e);
 }
 
 #define SCREE_DISPATCH(FN, dtype, D, causal, ...)                                 \
@@ -887,30 +936,84 @@ extern "C" int scree_attn_fwd(const void* q, const void* k, const void* v, void*
   return check_launch(fn);
 }
 
+static int check_bwd_tensors(const char* fn, const char* const* names, const void* const* ptrs,
+                             int n, const int64_t* strides, int heads, int head_dim,
+                             int64_t total) {
+  if (!strides) return set_error(SCREE_ERR_INVALID, "%s: strides is null", fn);
+  for (int i = 0; i < n; ++i) {
+    int rc = check_tensor(fn, names[i], ptrs[i], strides + 2 * i, heads, head_dim, total);
+    if (rc) return rc;
+  }
+  return SCREE_OK;
+}
+
+extern "C" int scree_attn_bwd_dq(const void* dout, const void* q, const void* k, const void* v,
+                                 const void* o, const float* lse, void* dq, float* delta,
+                                 const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                                 int heads, int head_dim, const int64_t* strides,
+                                 float softmax_scale, int causal, int dtype,
+                                 const void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "scree_attn_bwd_dq";
+  int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
+                        workspace_bytes);
+  if (rc) return rc;
+  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  if (!delta || !aligned16(delta))
+    return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
+  const char* names[6] = {"dout", "q", "k", "v", "o", "dq"};
+  const void* ptrs[6] = {dout, q, k, v, o, dq};
+  rc = check_bwd_tensors(fn, names, ptrs, 6, strides, heads, head_dim, total_tokens);
+  if (rc) return rc;
+  if (total_tokens == 0) return SCREE_OK;
+  const int64_t grid = tmax_for(batch, total_tokens) * heads;
+  SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
+                 cu_seqlens, heads, strides, softmax_scale, grid, workspace,
+                 static_cast<hipStream_t>(stream));
+  return check_launch(fn);
+}
+
+extern "C" int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k, const void* v,
+                                  const float* lse, const float* delta, void* dk, void* dv,
+                                  const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                                  int heads, int head_dim, const int64_t* strides,
+                                  float softmax_scale, int causal, int dtype,
+                                  const void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "scree_attn_bwd_dkv";
+  int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
+                        workspace_bytes);
+  if (rc) return rc;
+  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  if (!delta || !aligned16(delta))
+    return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
+  const char* names[6] = {"dout", "q", "k", "v", "dk", "dv"};
+  const void* ptrs[6] = {dout, q, k, v, dk, dv};
+  rc = check_bwd_tensors(fn, names, ptrs, 6, strides, heads, head_dim, total_tokens);
+  if (rc) return rc;
+  if (total_tokens == 0) return SCREE_OK;
+  const int64_t grid = tmax_for(batch, total_tokens) * heads;
+  SCREE_DISPATCH(launch_bwd_dkv_t, dtype, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
+                 cu_seqlens, heads, strides, softmax_scale, grid, workspace,
+                 static_cast<hipStream_t>(stream));
+  return check_launch(fn);
+}
+
 extern "C" int scree_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
                               const void* o, const float* lse, void* dq, void* dk, void* dv,
                               float* delta, const int32_t* cu_seqlens, int batch,
                               int64_t total_tokens, int heads, int head_dim,
                               const int64_t* strides, float softmax_scale, int causal, int dtype,
                               const void* workspace, size_t workspace_bytes, void* stream) {
-  const char* fn = "scree_attn_bwd";
-  int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
-                        workspace_bytes);
+  if (!strides) return set_error(SCREE_ERR_INVALID, "scree_attn_bwd: strides is null");
+  // strides: {dout, q, k, v, o, dq, dk, dv} x {row, head}
+  const int64_t sdq[12] = {strides[0], strides[1], strides[2], strides[3], strides[4], strides[5],
+                           strides[6], strides[7], strides[8], strides[9], strides[10], strides[11]};
+  const int64_t sdkv[12] = {strides[0], strides[1], strides[2],  strides[3],  strides[4],  strides[5],
+                            strides[6], strides[7], strides[12], strides[13], strides[14], strides[15]};
+  int rc = scree_attn_bwd_dq(dout, q, k, v, o, lse, dq, delta, cu_seqlens, batch, total_tokens,
+                             heads, head_dim, sdq, softmax_scale, causal, dtype, workspace,
+                             workspace_bytes, stream);
   if (rc) return rc;
-  if (!strides) return set_error(SCREE_ERR_INVALID, "%s: strides is null", fn);
-  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
-  if (!delta || !aligned16(delta))
-    return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
-  const char* names[8] = {"dout", "q", "k", "v", "o", "dq", "dk", "dv"};
-  const void* ptrs[8] = {dout, q, k, v, o, dq, dk, dv};
-  for (int i = 0; i < 8; ++i) {
-    rc = check_tensor(fn, names[i], ptrs[i], strides + 2 * i, heads, head_dim, total_tokens);
-    if (rc) return rc;
-  }
-  if (total_tokens == 0) return SCREE_OK;
-  const int64_t grid = tmax_for(batch, total_tokens) * heads;
-  SCREE_DISPATCH(launch_bwd_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, dk, dv, delta,
-                 cu_seqlens, heads, strides, softmax_scale, grid, workspace,
-                 static_cast<hipStream_t>(stream));
-  return check_launch(fn);
+  return scree_attn_bwd_dkv(dout, q, k, v, lse, delta, dk, dv, cu_seqlens, batch, total_tokens,
+                            heads, head_dim, sdkv, softmax_scale, causal, dtype, workspace,
+                            workspace_bytes, stream);
 }

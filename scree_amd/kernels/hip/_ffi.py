@@ -38,6 +38,10 @@ _SIGNATURES = {
     "scree_attn_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I, _P, _S, _P]),
     "scree_attn_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I,
                             _P, _S, _P]),
+    "scree_attn_bwd_dq": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I, _P,
+                               _S, _P]),
+    "scree_attn_bwd_dkv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I, _P,
+                                _S, _P]),
     "scree_norm_bwd_workspace_bytes": (_S, [_L, _L]),
     "scree_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _L, _L, _F, _I, _P]),
     "scree_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),

@@ -117,6 +117,28 @@ def _attn_bwd(do, q, k, v, o, lse, cu, causal, dq, dk, dv, delta, workspace):
         _ffi.stream_of(q)))
 
 
+def _attn_bwd_dq(do, q, k, v, o, lse, cu, causal, dq, delta, workspace):
+    lib = _ffi.lib()
+    total, heads, head_dim = q.shape
+    strides = _ffi.int64_array([s for t in (do, q, k, v, o, dq) for s in (t.stride(0), t.stride(1))])
+    _ffi.check(lib.scree_attn_bwd_dq(
+        _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(o), _ffi.ptr(lse),
+        _ffi.ptr(dq), _ffi.ptr(delta), _ffi.ptr(cu), cu.numel() - 1, total, heads, head_dim,
+        strides, 1.0 / math.sqrt(head_dim), int(bool(causal)), _ffi.dtype_code(q.dtype),
+        _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(q)))
+
+
+def _attn_bwd_dkv(do, q, k, v, lse, delta, cu, causal, dk, dv, workspace):
+    lib = _ffi.lib()
+    total, heads, head_dim = q.shape
+    strides = _ffi.int64_array([s for t in (do, q, k, v, dk, dv) for s in (t.stride(0), t.stride(1))])
+    _ffi.check(lib.scree_attn_bwd_dkv(
+        _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(lse), _ffi.ptr(delta),
+        _ffi.ptr(dk), _ffi.ptr(dv), _ffi.ptr(cu), cu.numel() - 1, total, heads, head_dim,
+        strides, 1.0 / math.sqrt(head_dim), int(bool(causal)), _ffi.dtype_code(q.dtype),
+        _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(q)))
+
+
 def varlen_attention_hip(q, k, v, cu_seqlens, causal: bool = False, block_m: int = 64,
                          block_n: int = 64, return_lse: bool = False, out=None, lse_buffer=None,
                          workspace=None):
