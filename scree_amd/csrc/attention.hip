@@ -337,8 +337,14 @@ struct Strides {
 constexpr float kRescaleLog2Gap = 8.0f;
 
 // ---------------------------------------------------------------- forward
+// Waves per SIMD the compiler must fit (it caps registers at 512 / this).
+template <int D>
+constexpr int fwd_waves_per_simd() {
+  return 2;
+}
+
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
+__global__ __launch_bounds__(kThreads, fwd_waves_per_simd<D>()) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, const int32_t* __restrict__ header, const int4* __restrict__ items,
     int heads, Strides sq, Strides sk, Strides sv, Strides so, float scale, float scale_log2) {
