@@ -155,6 +155,8 @@ def time_norms(cfg, steps, warmup):
         "layernorm_fwd": (lambda: Nm.layernorm_fwd(x, w, b, cfg.eps, True), lfb),
         "layernorm_bwd": (lambda: Nm.layernorm_bwd(dy, x, w, mean, lrstd, True, True, p_like=w), lbb),
     }
+    y = torch.empty_like(x)
+    cases["device_copy_same_bytes"] = (lambda: y.copy_(x), 2.0 * x.numel() * x.element_size())
     out = {}
     for name, (fn, nbytes) in cases.items():
         for _ in range(warmup):

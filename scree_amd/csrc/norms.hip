@@ -25,7 +25,6 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int kFwdWaves = 4;       // rows (waves) per forward block
-constexpr int kBwdWaves = 8;       // waves per backward block
 constexpr int kMaxParts = 512;     // partial rows of a backward, at most
 constexpr int kMaxChunks = 16;     // 16-byte vectors per lane on the fast path
 
@@ -44,7 +43,7 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int vi = c * kWave + lane;
-    v[c] = vi < nvec ? ld16(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+    v[c] = vi < nvec ? ld16_nt(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
   }
   const float fdim = (float)dim;
   float mu = 0.f, rstd;
@@ -94,7 +93,7 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
         if (LAYER && b) t += elem<T>(bv, e);
         f[e] = t;
       }
-      st16(yr + (int64_t)vi * VEC, pack16<T>(f));
+      st16_nt(yr + (int64_t)vi * VEC, pack16<T>(f));
     }
   }
   if (lane == 0) {
@@ -145,118 +144,154 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_generic(
 }
 
 // ----------------------------------------------------------------- backward
+// Column-ownership layout.  A block of kBwdThreads threads takes a contiguous
+// range of rows; thread t owns the 16-byte column vectors t + k*kBwdThreads
+// (k < CPT) of every row in it.  Per step of R rows the thread loads its
+// vectors of x and dy, the row statistics (sum x*g for RMS; sum g and
+// sum g*xhat for LN) are reduced across the wave by shuffles and across the
+// block through a double-buffered LDS array (one barrier per step), then the
+// thread writes dx for its vectors and adds its parameter gradients into
+// fp32 registers.  At the end each thread writes its own columns of the
+// block's partial row: no intra-block reduction, and the partial rows are
+// summed by norm_param_colsum in a fixed order.
 // partial layout: [part][param][dim] fp32, param 0 = dweight, 1 = dbias.
-template <typename T, int CHUNKS, bool LAYER>
-__global__ __launch_bounds__(kBwdWaves* kWave) void norm_bwd_vec(
+constexpr int kBwdThreads = 512;
+constexpr int kBwdWarps = kBwdThreads / kWave;
+
+template <typename T, int CPT, int R, bool LAYER>
+__global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ dx,
-    float* __restrict__ partial, int64_t rows, int dim, int nparam) {
+    float* __restrict__ partial, int64_t rows, int dim, int nparam, int64_t rows_per_block) {
   constexpr int VEC = 16 / sizeof(T);
-  extern __shared__ float red[];  // dim floats
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  __shared__ float red[2][R][2][kBwdWarps];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int nvec = dim / VEC;
   const float fdim = (float)dim;
-  float aw[CHUNKS][VEC];
-  float ab[LAYER ? CHUNKS : 1][VEC];
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = min(rows, r0 + rows_per_block);
+
+  uint4 wv[CPT];
+  bool own[CPT];
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c)
+  for (int k = 0; k < CPT; ++k) {
+    const int v = tid + k * kBwdThreads;
+    own[k] = v < nvec;
+    wv[k] = (w && own[k]) ? ld16(w + (int64_t)v * VEC) : make_uint4(0, 0, 0, 0);
+  }
+  float aw[CPT][VEC], ab[LAYER ? CPT : 1][VEC];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      aw[c][e] = 0.f;
-      if (LAYER) ab[LAYER ? c : 0][e] = 0.f;
+      aw[k][e] = 0.f;
+      ab[LAYER ? k : 0][e] = 0.f;
     }
 
-  for (int64_t row = (int64_t)blockIdx.x * kBwdWaves + wave; row < rows;
-       row += (int64_t)gridDim.x * kBwdWaves) {
-    const T* xr = x + row * (int64_t)dim;
-    const T* gr = dy + row * (int64_t)dim;
-    uint4 xv[CHUNKS], gv[CHUNKS];
+  int buf = 0;
+  for (int64_t rb = r0; rb < r1; rb += R) {
+    uint4 xv[R][CPT], gv[R][CPT];
+    float rs[R], mu[R];
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int vi = c * kWave + lane;
-      xv[c] = vi < nvec ? ld16(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
-      gv[c] = vi < nvec ? ld16(gr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
-    }
-    const float r = rstd_in[row];
-    const float mu = LAYER ? mean_in[row] : 0.f;
-    float s1 = 0.f, s2 = 0.f;
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = rb + r;
+      const bool ok = row < r1;
+      rs[r] = ok ? rstd_in[row] : 0.f;
+      mu[r] = (LAYER && ok) ? mean_in[row] : 0.f;
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int vi = c * kWave + lane;
-      if (vi < nvec) {
-        uint4 wv = make_uint4(0, 0, 0, 0);
-        if (w) wv = ld16(w + (int64_t)vi * VEC);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float xx = elem<T>(xv[c], e);
-          const float d = elem<T>(gv[c], e);
-          const float g = w ? d * elem<T>(wv, e) : d;
-          if (LAYER) {
-            const float xh = (xx - mu) * r;
-            s1 += g;
-            s2 += g * xh;
-            aw[c][e] += d * xh;
-            ab[LAYER ? c : 0][e] += d;
-          } else {
-            s1 += xx * g;
-            aw[c][e] += d * xx * r;
-          }
-        }
+      for (int k = 0; k < CPT; ++k) {
+        const int64_t off = row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC;
+        xv[r][k] = (ok && own[k]) ? ld16_nt(x + off) : make_uint4(0, 0, 0, 0);
+        gv[r][k] = (ok && own[k]) ? ld16_nt(dy + off) : make_uint4(0, 0, 0, 0);
       }
     }
-    s1 = wave_sum(s1);
-    if (LAYER) s2 = wave_sum(s2);
-    const float k_rms = r * r * r * s1 / fdim;
-    const float a_ln = s1 / fdim;
-    const float b_ln = s2 / fdim;
-    T* dxr = dx + row * (int64_t)dim;
+    float s1[R], s2[R];
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int vi = c * kWave + lane;
-      if (vi < nvec) {
-        uint4 wv = make_uint4(0, 0, 0, 0);
-        if (w) wv = ld16(w + (int64_t)vi * VEC);
+    for (int r = 0; r < R; ++r) {
+      s1[r] = 0.f;
+      s2[r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float xx = elem<T>(xv[r][k], e);
+          const float d = elem<T>(gv[r][k], e);
+          const float g = w ? d * elem<T>(wv[k], e) : d;
+          if (LAYER) {
+            s1[r] += g;
+            s2[r] += g * ((xx - mu[r]) * rs[r]);
+          } else {
+            s1[r] += xx * g;
+          }
+        }
+      s1[r] = wave_sum(s1[r]);
+      if (LAYER) s2[r] = wave_sum(s2[r]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        red[buf][r][0][wave] = s1[r];
+        red[buf][r][1][wave] = s2[r];
+      }
+    }
+    __syncthreads();
+    // Keep x and dy packed across the barrier: re-derive the fp32 values
+    // below instead of holding 2*R*CPT*VEC converted floats live.
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        asm volatile("" : "+v"(xv[r][k].x), "+v"(xv[r][k].y), "+v"(xv[r][k].z), "+v"(xv[r][k].w));
+        asm volatile("" : "+v"(gv[r][k].x), "+v"(gv[r][k].y), "+v"(gv[r][k].z), "+v"(gv[r][k].w));
+      }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+      for (int q = 0; q < kBwdWarps; ++q) {
+        t1 += red[buf][r][0][q];
+        if (LAYER) t2 += red[buf][r][1][q];
+      }
+      const int64_t row = rb + r;
+      if (row >= r1) continue;
+      const float k_rms = rs[r] * rs[r] * rs[r] * t1 / fdim;
+      const float a_ln = t1 / fdim, b_ln = t2 / fdim;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        if (!own[k]) continue;
         float f[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          const float xx = elem<T>(xv[c], e);
-          const float d = elem<T>(gv[c], e);
-          const float g = w ? d * elem<T>(wv, e) : d;
+          const float xx = elem<T>(xv[r][k], e);
+          const float d = elem<T>(gv[r][k], e);
+          const float g = w ? d * elem<T>(wv[k], e) : d;
           if (LAYER) {
-            const float xh = (xx - mu) * r;
-            f[e] = r * (g - a_ln - xh * b_ln);
+            const float xh = (xx - mu[r]) * rs[r];
+            f[e] = rs[r] * (g - a_ln - xh * b_ln);
+            aw[k][e] += d * xh;
+            ab[LAYER ? k : 0][e] += d;
           } else {
-            f[e] = r * g - k_rms * xx;
+            f[e] = rs[r] * g - k_rms * xx;
+            aw[k][e] += d * xx * rs[r];
           }
         }
-        st16(dxr + (int64_t)vi * VEC, pack16<T>(f));
+        st16_nt(dx + row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC, pack16<T>(f));
       }
     }
+    buf ^= 1;
   }
-
-  // Fixed-order block reduction of the per-wave parameter partials.
   for (int p = 0; p < nparam; ++p) {
-    for (int turn = 0; turn < kBwdWaves; ++turn) {
-      if (wave == turn) {
-#pragma unroll
-        for (int c = 0; c < CHUNKS; ++c) {
-          const int vi = c * kWave + lane;
-          if (vi < nvec) {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-              const float a = (p == 0) ? aw[c][e] : ab[LAYER ? c : 0][e];
-              const int idx = vi * VEC + e;
-              red[idx] = turn == 0 ? a : red[idx] + a;
-            }
-          }
-        }
-      }
-      __syncthreads();
-    }
     float* out = partial + ((int64_t)blockIdx.x * nparam + p) * dim;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = red[i];
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      if (!own[k]) continue;
+      float* o = out + (int64_t)(tid + k * kBwdThreads) * VEC;
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4) {
+        const float* src = p == 0 ? &aw[k][e] : &ab[LAYER ? k : 0][e];
+        *reinterpret_cast<float4*>(o + e) = make_float4(src[0], src[1], src[2], src[3]);
+      }
+    }
   }
 }
 
@@ -327,7 +362,14 @@ __global__ __launch_bounds__(256) void norm_bwd_param_generic(
   if (nparam > 1) out[dim + col] = ab;
 }
 
-// Column sums of the partial rows, in part order; output cast to out_dtype.
+// Column sums of the partial rows; output cast to out_dtype.  Scalar form
+// (any dim): 64 columns x 4 row groups per block.
+__device__ __forceinline__ void store_param(void* out, int col, float t, int out_dtype) {
+  if (out_dtype == SCREE_DTYPE_F32) static_cast<float*>(out)[col] = t;
+  else if (out_dtype == SCREE_DTYPE_F16) static_cast<f16*>(out)[col] = (f16)t;
+  else static_cast<bf16*>(out)[col] = (bf16)t;
+}
+
 __global__ __launch_bounds__(256) void norm_param_colsum(const float* __restrict__ partial,
                                                          int nparts, int nparam, int dim,
                                                          void* out0, void* out1, int out_dtype) {
@@ -345,11 +387,45 @@ __global__ __launch_bounds__(256) void norm_param_colsum(const float* __restrict
   if (grp == 0 && col < dim) {
     const float t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
     void* out = p == 0 ? out0 : out1;
-    if (out) {
-      if (out_dtype == SCREE_DTYPE_F32) static_cast<float*>(out)[col] = t;
-      else if (out_dtype == SCREE_DTYPE_F16) static_cast<f16*>(out)[col] = (f16)t;
-      else static_cast<bf16*>(out)[col] = (bf16)t;
+    if (out) store_param(out, col, t, out_dtype);
+  }
+}
+
+// Vector form (dim % 4 == 0): 16 columns x 64 row groups per block, 16-byte
+// loads, then a fixed-order tree over the row groups in LDS (deterministic).
+__global__ __launch_bounds__(256) void norm_param_colsum4(const float* __restrict__ partial,
+                                                          int nparts, int nparam, int dim,
+                                                          void* out0, void* out1, int out_dtype) {
+  __shared__ float4 red[64][4];
+  const int cq = threadIdx.x & 3, rg = threadIdx.x >> 2;
+  const int col = blockIdx.x * 16 + cq * 4;
+  const int p = blockIdx.y;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (col < dim) {
+#pragma unroll 4
+    for (int i = rg; i < nparts; i += 64) {
+      const float4 v = *reinterpret_cast<const float4*>(partial + ((int64_t)i * nparam + p) * dim + col);
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
+  }
+  red[rg][cq] = s;
+  __syncthreads();
+  for (int st = 32; st >= 1; st >>= 1) {
+    if (rg < st) {
+      const float4 o = red[rg + st][cq];
+      float4 m = red[rg][cq];
+      m.x += o.x; m.y += o.y; m.z += o.z; m.w += o.w;
+      red[rg][cq] = m;
+    }
+    __syncthreads();
+  }
+  void* out = p == 0 ? out0 : out1;
+  if (rg == 0 && col < dim && out) {
+    const float4 t = red[0][cq];
+    store_param(out, col + 0, t.x, out_dtype);
+    store_param(out, col + 1, t.y, out_dtype);
+    store_param(out, col + 2, t.z, out_dtype);
+    store_param(out, col + 3, t.w, out_dtype);
   }
 }
 
@@ -364,7 +440,7 @@ inline int chunks_for(int nvec) {
 }
 
 inline int nparts_for(int64_t rows) {
-  int64_t p = (rows + kBwdWaves - 1) / kBwdWaves;
+  int64_t p = (rows + 7) / 8;
   if (p < 1) p = 1;
   if (p > kMaxParts) p = kMaxParts;
   return (int)p;
@@ -378,6 +454,24 @@ bool fast_path_ok(int64_t dim, std::initializer_list<const void*> ptrs) {
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return false;
   return true;
+}
+
+// Backward fast path: whole 16-byte vectors, at most 2 per thread of a 512-thread block.
+template <typename T>
+bool bwd_fast_path_ok(int64_t dim, std::initializer_list<const void*> ptrs) {
+  constexpr int VEC = 16 / sizeof(T);
+  if (dim % VEC) return false;
+  if (dim / VEC > 2 * (int64_t)kBwdThreads) return false;
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return false;
+  return true;
+}
+
+// Rows per backward block: nparts blocks cover all rows in multiples of 8
+// (a multiple of every row step R the kernel is instantiated with).
+inline int64_t rows_per_part(int64_t rows, int nparts) {
+  int64_t r = (rows + nparts - 1) / nparts;
+  return ((r + 7) / 8) * 8;
 }
 
 template <typename T, bool LAYER>
@@ -427,26 +521,21 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* mean, 
   const bool want_params = (dw != nullptr) || (db != nullptr);
   const int nparts = nparts_for(rows);
   float* partial = static_cast<float*>(workspace);
-  if (fast_path_ok<T>(dim, {dy, x, w, dx})) {
-    const int chunks = chunks_for((int)(dim / (16 / sizeof(T))));
-    const dim3 grid((unsigned)nparts), block(kBwdWaves * kWave);
-    const size_t lds = (size_t)d * sizeof(float);
+  if (bwd_fast_path_ok<T>(dim, {dy, x, w, dx})) {
+    const int nvec = (int)(dim / (16 / sizeof(T)));
+    const int cpt = (nvec + kBwdThreads - 1) / kBwdThreads;  // 1 or 2
+    const int64_t rpb = rows_per_part(rows, nparts);
+    const dim3 grid((unsigned)nparts), block(kBwdThreads);
     const int np = want_params ? nparam : 0;
-#define SCREE_BWD_CASE(C)                                                                        \
-  case C:                                                                                        \
-    hipLaunchKernelGGL((norm_bwd_vec<T, C, LAYER>), grid, block, lds, stream, dyp, xp, wp, mean,  \
-                       rstd, dxp, partial, rows, d, np);                                         \
-    break;
-    switch (chunks) {
-      SCREE_BWD_CASE(1)
-      SCREE_BWD_CASE(2)
-      SCREE_BWD_CASE(4)
-      SCREE_BWD_CASE(8)
-      SCREE_BWD_CASE(16)
-      default:
-        return set_error(SCREE_ERR_INVALID, "norm backward: internal chunk count %d", chunks);
-    }
-#undef SCREE_BWD_CASE
+    // rows per step: as many as fit 4 waves per SIMD (LN keeps two sums per row)
+    constexpr int R1 = LAYER ? 4 : 8;
+    constexpr int R2 = LAYER ? 2 : 4;
+    if (cpt == 1)
+      hipLaunchKernelGGL((norm_bwd_cols<T, 1, R1, LAYER>), grid, block, 0, stream, dyp, xp, wp, mean,
+                         rstd, dxp, partial, rows, d, np, rpb);
+    else
+      hipLaunchKernelGGL((norm_bwd_cols<T, 2, R2, LAYER>), grid, block, 0, stream, dyp, xp, wp, mean,
+                         rstd, dxp, partial, rows, d, np, rpb);
   } else {
     const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves)), block(kFwdWaves * kWave);
     if (rows > 0)
@@ -460,9 +549,15 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* mean, 
   }
   int rc = check_launch(LAYER ? "scree_layernorm_bwd" : "scree_rmsnorm_bwd");
   if (rc != SCREE_OK || !want_params) return rc;
-  const dim3 cgrid((unsigned)((dim + kWave - 1) / kWave), (unsigned)nparam);
-  hipLaunchKernelGGL(norm_param_colsum, cgrid, dim3(256), 0, stream, partial, nparts, nparam, d, dw,
-                     db, dparam_dtype);
+  if (dim % 4 == 0) {
+    const dim3 cgrid((unsigned)((dim + 15) / 16), (unsigned)nparam);
+    hipLaunchKernelGGL(norm_param_colsum4, cgrid, dim3(256), 0, stream, partial, nparts, nparam, d,
+                       dw, db, dparam_dtype);
+  } else {
+    const dim3 cgrid((unsigned)((dim + kWave - 1) / kWave), (unsigned)nparam);
+    hipLaunchKernelGGL(norm_param_colsum, cgrid, dim3(256), 0, stream, partial, nparts, nparam, d,
+                       dw, db, dparam_dtype);
+  }
   return check_launch(LAYER ? "scree_layernorm_bwd (param sum)" : "scree_rmsnorm_bwd (param sum)");
 }
 
