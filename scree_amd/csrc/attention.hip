@@ -330,6 +330,32 @@ struct Strides {
   int64_t row, head;
 };
 
+// Workgroups are dispatched round-robin over the 8 XCDs (block b runs on XCD
+// b % 8), each with its own L2.  Two block -> (item, head) orders:
+//  * head-minor (block b -> item b / heads, head b % heads): every head's
+//    longest items start first -- best balance when each XCD has only a few
+//    rounds of work.  With heads a multiple of 8 each head still stays on one
+//    XCD.
+//  * head-major (heads a multiple of 8): XCD x works through heads x, x + 8,
+//    ... one at a time, each in the scheduler's longest-first order, so one
+//    head's K/V is the L2 working set -- best when each XCD has many rounds.
+// The host picks (attn_head_major).  Returns false for blocks past the work.
+constexpr int kXcds = 8;
+__device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, int& item,
+                                          int& head) {
+  const int b = blockIdx.x;
+  if (head_major) {
+    const int x = b % kXcds, j = b / kXcds;
+    const int k = j / tmax;  // k-th head of this XCD
+    item = j - k * tmax;
+    head = x + kXcds * k;
+    return head < heads;
+  }
+  item = b / heads;
+  head = b % heads;
+  return true;
+}
+
 // A softmax row's reference maximum is raised only when the block maximum
 // exceeds it by more than this many powers of two; p = 2^(s*c - m*c) then
 // stays <= 2^8, which fp32 sums and fp16/bf16 operands hold exactly as well
@@ -337,146 +363,226 @@ struct Strides {
 constexpr float kRescaleLog2Gap = 8.0f;
 
 // ---------------------------------------------------------------- forward
-// Waves per SIMD the compiler must fit (it caps registers at 512 / this).
+// Direct-to-LDS tiles.  A ROWS x D tile of one head is copied from HBM into
+// an unpadded row-major LDS tile by buffer loads with an LDS destination
+// (no registers in between): each wave instruction fills one contiguous
+// 1 KB window, lane l writing bytes [16 l, 16 l + 16), so the tile's layout is
+// chosen by which global chunk each lane fetches.  The 16-byte chunk c of row
+// r is stored at chunk position c ^ swz(r); with swz below, both the 16-byte
+// row reads (8 consecutive rows, one chunk) and the transposed 8-byte reads
+// (4 consecutive rows, two adjacent chunks) touch 32 distinct banks.  The
+// buffer descriptor covers only the sequence's valid rows: rows past it are
+// written as zeros by the hardware.
 template <int D>
-constexpr int fwd_waves_per_simd() {
-  return 2;
+__device__ __forceinline__ int swz(int row) {
+  return D >= 64 ? 2 * (row & 3) + ((row >> 2) & 1) : 2 * ((row >> 1) & 1) + ((row >> 2) & 1);
+}
+
+template <typename T, int D, int ROWS>
+struct DmaTile {
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int RPI = 1024 / (D * 2);        // rows per wave instruction
+  static constexpr int INSTR = ROWS * D * 2 / 1024; // wave instructions per tile
+  static_assert(INSTR % 4 == 0, "tile must split evenly over the 4 waves");
+  static constexpr int PER_WAVE = INSTR / 4;
+  uint32_t voff[PER_WAVE];
+
+  __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int q = i * 4 + wave;
+      const int r = q * RPI + lane / CPR;
+      const int c = (lane % CPR) ^ swz<D>(r);
+      voff[i] = (uint32_t)(((int64_t)r * row_stride + c * 8) * (int64_t)sizeof(T));
+    }
+  }
+  // rows [row0, row0 + ROWS) of a sequence starting at `base` into `lds`
+  // (ROWS * D elements); rows >= limit become zeros.
+  __device__ __forceinline__ void load(T* lds, const T* __restrict__ base, int64_t row_stride,
+                                       int row0, int limit, int wave) const {
+    const int valid = min(ROWS, limit - row0);
+    const uint32_t bytes = valid > 0 ? (uint32_t)((int64_t)valid * row_stride * (int64_t)sizeof(T)) : 0u;
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS address-space cast exists only on the device side
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)row0 * row_stride, bytes);
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int q = i * 4 + wave;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(lds + q * 512), 16, voff[i], 0, 0, 0);
+    }
+#endif
+  }
+};
+
+// Element offset, inside a swizzled tile, of this lane's row-read fragment
+// (row `row`, logical chunk `c`).
+template <int D>
+__device__ __forceinline__ int swz_off(int row, int c) {
+  return row * D + ((c ^ swz<D>(row)) << 3);
+}
+// This lane's transposed-read offset for column block dt (32 columns): the
+// lane addresses row 4g + (lr%16)/4, column 32dt + 16(lr/16) + 4(lr%4)
+// (see lds_frag_tr); the second read, 8 rows down, has the same swizzle.
+template <int D>
+__device__ __forceinline__ int swz_tr_off(int lr, int g, int dt) {
+  const int r = 4 * g + ((lr & 15) >> 2);
+  const int c = 4 * dt + 2 * (lr >> 4) + ((lr & 3) >> 1);
+  return r * D + ((c ^ swz<D>(r)) << 3) + 4 * (lr & 1);
+}
+
+// Per-wave state of the forward loop over 64-key blocks.
+template <typename T, int D>
+struct FwdState {
+  typedef typename VecT<T>::x8 x8;
+  x8 qf[D / 16];            // this lane's query row, MFMA B fragments
+  int koff[D / 16];         // swizzled K row-read offsets
+  int voffs[D / 32];        // swizzled V transposed-read offsets
+  f32x16 oacc[D / 32];      // O^T accumulators
+  float m_run, l_run;       // running max (raw scores) and row sum
+  DmaTile<T, D, kBN> dK, dV;
+  const T* kh;
+  const T* vh;
+  int64_t krow, vrow;
+  int L, nkb, kend_wave, qw0, wave, lr, g;
+  float scale_log2, rescale_gap;
+};
+
+// One 64-key block: start the DMA of block kb+1 into `nxt`, then compute on
+// `cur` (K tile, then V tile). The restrict qualifiers tell the compiler the
+// two buffers are disjoint, so it keeps the DMA in flight across the reads.
+template <typename T, int D, bool CAUSAL>
+__device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* __restrict__ cur,
+                                          T* __restrict__ nxt) {
+  typedef typename VecT<T>::x8 x8;
+  constexpr int TILE = kBN * D;
+  const T* sK = cur;
+  const T* sV = cur + TILE;
+  if (kb + 1 < st.nkb) {
+    st.dK.load(nxt, st.kh, st.krow, (kb + 1) * kBN, st.L, st.wave);
+    st.dV.load(nxt + TILE, st.vh, st.vrow, (kb + 1) * kBN, st.L, st.wave);
+  }
+  const int kbase = kb * kBN;
+  const int nt = kbase < st.kend_wave ? (kbase + 32 < st.kend_wave ? 2 : 1) : 0;
+  f32x16 snext;
+  if (nt > 0) {
+    snext = zero16();
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) snext = mfma32(lds_frag16(sK + st.koff[s]), st.qf[s], snext);
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (t >= nt) break;
+    f32x16 sacc = snext;
+    if (t + 1 < nt) {  // issue the next tile's scores before this tile's softmax
+      snext = zero16();
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s)
+        snext = mfma32(lds_frag16(sK + 32 * D + st.koff[s]), st.qf[s], snext);
+    }
+    const int tbase = kbase + 32 * t;
+    if (CAUSAL) {
+      if (tbase == st.qw0) mask_rows_above(sacc, st.lr - 4 * st.g);  // the diagonal tile
+    } else if (tbase + 32 > st.L) {
+      mask_rows_above(sacc, st.L - 1 - tbase - 4 * st.g);
+    }
+    float mx = sacc[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const bool grow = mx > st.m_run + st.rescale_gap;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : st.m_run;
+      const float alpha = fast_exp2((st.m_run - m_new) * st.scale_log2);
+      st.l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.oacc[dt][i] *= alpha;
+      st.m_run = m_new;
+    }
+    const float mb = st.m_run == kNegInf ? 0.f : st.m_run * st.scale_log2;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = fast_exp2(fmaf(sacc[i], st.scale_log2, -mb));
+      sacc[i] = p;
+      st.l_run += p;
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const x8 pf = pack_frag<T>(sacc, 8 * hh);
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+        st.oacc[dt] = mfma32(lds_frag_tr(sV + (32 * t + 16 * hh) * D + st.voffs[dt], D), pf,
+                             st.oacc[dt]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block kb+1 has landed
+  __syncthreads();
 }
 
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, fwd_waves_per_simd<D>()) void attn_fwd_kernel(
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, const int32_t* __restrict__ header, const int4* __restrict__ items,
-    int heads, Strides sq, Strides sk, Strides sv, Strides so, float scale, float scale_log2) {
-  constexpr int KLD = D + 8;    // sK leading dim: 16-byte pad, row reads conflict-free
-  constexpr int VLD = D + 16;   // sV leading dim: 32-byte pad, transposed reads conflict-free
-  constexpr int BUF = kBN * KLD + kBN * VLD;
-  __shared__ __align__(16) T smem[2 * BUF];
+    int tmax, int head_major, int heads, Strides sq, Strides sk, Strides sv, Strides so,
+    float scale, float scale_log2) {
+  constexpr int TILE = kBN * D;  // elements per K or V tile
+  // Two distinct arrays (K then V in each), alternated at compile-time
+  // positions of the loop below.
+  __shared__ __align__(16) T bufA[2 * TILE];
+  __shared__ __align__(16) T bufB[2 * TILE];
 
-  const int item = blockIdx.x / heads, h = blockIdx.x % heads;
-  if (item >= header[0]) return;
+  int item, h;
+  if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
   const int4 it = items[item];
   const int start = it.z, L = it.w, q0 = it.y * kBM;
-  const int wave = wave_id(), lane = threadIdx.x & (kWave - 1);
-  const int g = lane >> 5, lr = lane & 31;
-  const int qw0 = q0 + 32 * wave;
-  const int my_q = qw0 + lr;
-  const bool wave_live = qw0 < L;
+  FwdState<T, D> st;
+  st.wave = wave_id();
+  const int lane = threadIdx.x & (kWave - 1);
+  st.g = lane >> 5;
+  st.lr = lane & 31;
+  st.qw0 = q0 + 32 * st.wave;
+  const int my_q = st.qw0 + st.lr;
+  const bool wave_live = st.qw0 < L;
+  st.L = L;
+  st.kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
+  st.vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
+  st.krow = sk.row;
+  st.vrow = sv.row;
+  const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
+  st.nkb = (kend_wg + kBN - 1) / kBN;
+  st.kend_wave = wave_live ? (CAUSAL ? min(L, st.qw0 + 32) : L) : 0;
 
-  const T* kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
-  const T* vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
+  st.dK.init(sk.row, st.wave, lane);
+  st.dV.init(sv.row, st.wave, lane);
+  st.dK.load(bufA, st.kh, sk.row, 0, L, st.wave);
+  st.dV.load(bufA + TILE, st.vh, sv.row, 0, L, st.wave);
 
-  typedef typename VecT<T>::x8 x8;
-  x8 qf[D / 16];
   {  // rows past L read row L-1: their results are never stored
     const T* qrow = q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
+    for (int s = 0; s < D / 16; ++s) st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
   }
-
-  const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
-  const int nkb = (kend_wg + kBN - 1) / kBN;
-  const int kend_wave = wave_live ? (CAUSAL ? min(L, qw0 + 32) : L) : 0;
-  const float rescale_gap = kRescaleLog2Gap / scale_log2;
-
-  f32x16 oacc[D / 32];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = zero16();
-  float m_run = kNegInf, l_run = 0.f;
+  for (int s = 0; s < D / 16; ++s) st.koff[s] = swz_off<D>(st.lr, 2 * s + st.g);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) st.voffs[dt] = swz_tr_off<D>(st.lr, st.g, dt);
+  st.scale_log2 = scale_log2;
+  st.rescale_gap = kRescaleLog2Gap / scale_log2;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) st.oacc[dt] = zero16();
+  st.m_run = kNegInf;
+  st.l_run = 0.f;
 
-  Stage<T, D, kBN> stK, stV;
-  stK.init(sk.row);
-  stV.init(sv.row);
-  stK.load(kh, sk.row, 0, L);
-  stV.load(vh, sv.row, 0, L);
-  stK.put_rows(smem, KLD);
-  stV.put_rows(smem + kBN * KLD, VLD);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int vtr = tr_lane_offset(lr, g, VLD);
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const T* sK = smem + (kb & 1) * BUF;
-    const T* sV = sK + kBN * KLD;
-    if (kb + 1 < nkb) {
-      stK.load(kh, sk.row, (kb + 1) * kBN, L);
-      stV.load(vh, sv.row, (kb + 1) * kBN, L);
-    }
-    const int kbase = kb * kBN;
-    const int nt = kbase < kend_wave ? (kbase + 32 < kend_wave ? 2 : 1) : 0;
-    if (nt > 0) {
-      f32x16 sacc[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (t < nt) {
-          sacc[t] = zero16();
-#pragma unroll
-          for (int s = 0; s < D / 16; ++s)
-            sacc[t] = mfma32(lds_frag16(sK + (32 * t + lr) * KLD + 16 * s + 8 * g), qf[s], sacc[t]);
-        }
-      }
-      if (CAUSAL) {
-        // only the tile starting at qw0 straddles the diagonal: keys > my_q
-        if (kbase + 32 * (nt - 1) == qw0) {
-          if (nt == 1) mask_rows_above(sacc[0], lr - 4 * g);
-          else mask_rows_above(sacc[1], lr - 4 * g);
-        }
-      } else if (kbase + 32 * nt > L) {
-        // keys >= L hold zeros; drop them from the softmax
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          if (t < nt) mask_rows_above(sacc[t], L - 1 - (kbase + 32 * t) - 4 * g);
-      }
-      float mx = kNegInf;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        if (t < nt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[t][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const bool grow = mx > m_run + rescale_gap;
-      if (__any(grow)) {
-        const float m_new = grow ? mx : m_run;
-        const float alpha = fast_exp2((m_run - m_new) * scale_log2);
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
-        m_run = m_new;
-      }
-      const float mb = m_run == kNegInf ? 0.f : m_run * scale_log2;
-      float psum = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        if (t < nt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float p = fast_exp2(fmaf(sacc[t][i], scale_log2, -mb));
-            sacc[t][i] = p;
-            psum += p;
-          }
-      l_run += psum;
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (t < nt) {
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const x8 pf = pack_frag<T>(sacc[t], 8 * hh);
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt)
-              oacc[dt] = mfma32(lds_frag_tr(sV + vtr + (32 * t + 16 * hh) * VLD + 32 * dt, VLD), pf,
-                                oacc[dt]);
-          }
-        }
-      }
-    }
-    if (kb + 1 < nkb) {
-      T* nK = smem + ((kb + 1) & 1) * BUF;
-      stK.put_rows(nK, KLD);
-      stV.put_rows(nK + kBN * KLD, VLD);
-    }
-    __syncthreads();
+  for (int kb = 0; kb < st.nkb; kb += 2) {
+    fwd_block<T, D, CAUSAL>(st, kb, bufA, bufB);
+    if (kb + 1 < st.nkb) fwd_block<T, D, CAUSAL>(st, kb + 1, bufB, bufA);
   }
+  const int g = st.g, lr = st.lr;
+  const float m_run = st.m_run, l_run = st.l_run;
+  const f32x16* oacc = st.oacc;
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   if (wave_live && my_q < L) {
@@ -506,15 +612,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
     float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
+    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
     Strides so, Strides sdq, float scale, float scale_log2) {
   constexpr int NBUF = dq_buffers<T, D>();
   constexpr int KLD = D + 8;
   constexpr int BUF = 2 * kBN * KLD;  // K rows, V rows
   __shared__ __align__(16) T smem[NBUF * BUF];
 
-  const int item = blockIdx.x / heads, h = blockIdx.x % heads;
-  if (item >= header[0]) return;
+  int item, h;
+  if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
   const int4 it = items[item];
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   const int wave = wave_id(), lane = threadIdx.x & (kWave - 1);
@@ -627,7 +733,7 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
     T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
+    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
     Strides sdk, Strides sdv, float scale, float scale_log2) {
   constexpr int BQ = D >= 128 ? 32 : 64;
   constexpr int NQT = BQ / 32;
@@ -636,8 +742,8 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
   __shared__ __align__(16) T smem[2 * BUF];
   __shared__ __align__(16) float sLD[2][2][BQ];  // [buffer][lse*log2e | delta][row]
 
-  const int item = blockIdx.x / heads, h = blockIdx.x % heads;
-  if (item >= header[0]) return;
+  int item, h;
+  if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
   const int4 it = items[item];
   const int start = it.z, L = it.w;
   const int nblk = (L + kBM - 1) / kBM;
@@ -821,15 +927,22 @@ int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, in
   return SCREE_OK;
 }
 
+// Head-major block order pays off once every XCD has many rounds of items
+// (~64 resident workgroups per XCD): then L2 locality beats cross-head balance.
+inline int attn_head_major(int heads, int tmax) {
+  return (heads % kXcds == 0) && ((int64_t)tmax * heads / kXcds >= 512) ? 1 : 0;
+}
+
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
-                  const int32_t* cu, int heads, const int64_t* st, float scale, int64_t grid,
+                  const int32_t* cu, int heads, const int64_t* st, float scale, int tmax,
                   const void* ws, hipStream_t stream) {
+  const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(o), lse, header, items, heads, Strides{st[0], st[1]},
+                     static_cast<T*>(o), lse, header, items, tmax, attn_head_major(heads, tmax), heads, Strides{st[0], st[1]},
                      Strides{st[2], st[3]}, Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale,
                      scale * kLog2e);
 }
@@ -838,15 +951,16 @@ void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* l
 template <typename T, int D, bool C>
 void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
                      const float* lse, void* dq, float* delta, const int32_t* cu, int heads,
-                     const int64_t* st, float scale, int64_t grid, const void* ws,
+                     const int64_t* st, float scale, int tmax, const void* ws,
                      hipStream_t stream) {
+  const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
   hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<const T*>(o), lse, delta, static_cast<T*>(dq), header, items,
-                     heads, Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
+                     tmax, attn_head_major(heads, tmax), heads, Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
                      scale * kLog2e);
 }
@@ -855,14 +969,15 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
 template <typename T, int D, bool C>
 void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
                       const float* lse, const float* delta, void* dk, void* dv, const int32_t* cu,
-                      int heads, const int64_t* st, float scale, int64_t grid, const void* ws,
+                      int heads, const int64_t* st, float scale, int tmax, const void* ws,
                       hipStream_t stream) {
+  const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
   hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0,
                      stream, static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), lse, delta,
-                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, heads,
+                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, tmax, attn_head_major(heads, tmax), heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
                      scale * kLog2e);
@@ -936,9 +1051,9 @@ extern "C" int scree_attn_fwd(const void* q, const void* k, const void* v, void*
     if (rc) return rc;
   }
   if (total_tokens == 0) return SCREE_OK;
-  const int64_t grid = tmax_for(batch, total_tokens) * heads;
+  const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, heads,
-                 strides, softmax_scale, grid, workspace, static_cast<hipStream_t>(stream));
+                 strides, softmax_scale, tmax, workspace, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
@@ -971,9 +1086,9 @@ extern "C" int scree_attn_bwd_dq(const void* dout, const void* q, const void* k,
   rc = check_bwd_tensors(fn, names, ptrs, 6, strides, heads, head_dim, total_tokens);
   if (rc) return rc;
   if (total_tokens == 0) return SCREE_OK;
-  const int64_t grid = tmax_for(batch, total_tokens) * heads;
+  const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
-                 cu_seqlens, heads, strides, softmax_scale, grid, workspace,
+                 cu_seqlens, heads, strides, softmax_scale, tmax, workspace,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
@@ -996,9 +1111,9 @@ extern "C" int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k
   rc = check_bwd_tensors(fn, names, ptrs, 6, strides, heads, head_dim, total_tokens);
   if (rc) return rc;
   if (total_tokens == 0) return SCREE_OK;
-  const int64_t grid = tmax_for(batch, total_tokens) * heads;
+  const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_bwd_dkv_t, dtype, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
-                 cu_seqlens, heads, strides, softmax_scale, grid, workspace,
+                 cu_seqlens, heads, strides, softmax_scale, tmax, workspace,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
