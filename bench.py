@@ -195,7 +195,19 @@ def time_autograd_step(cfg, dtype, steps, warmup):
     return {"ms": ms, "tflops": cfg.fwd_flops() * 3.5 / (ms * 1e-3) / 1e12}
 
 
-def cpu_baseline(cfg, heads_sample=2, iters=3):
+def _cpu_median(fn, warmup=2, iters=5) -> float:
+    """Median seconds of ``fn`` (time.perf_counter), after ``warmup`` untimed calls."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baseline(cfg, heads_sample=1, warmup=2, iters=5):
     """The oracle (reference numpy einsum path, fp32, single-threaded) on a head sample."""
     import numpy as np
 
@@ -212,13 +224,7 @@ def cpu_baseline(cfg, heads_sample=2, iters=3):
         o, lse = attention_fwd(q, k, v, off, causal=cfg.causal, dtype=np.float32, impl="einsum")
         attention_bwd(do, q, k, v, o, lse, off, causal=cfg.causal, dtype=np.float32, impl="einsum")
 
-    run()  # warmup
-    times = []
-    for _ in range(iters):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
+    sec = _cpu_median(run, warmup, iters)
     flops = 3.5 * workloads.attn_fwd_flops(cfg.lengths, heads_sample, d, cfg.causal)
     return {
         "value": flops / sec / 1e12,
@@ -227,10 +233,44 @@ def cpu_baseline(cfg, heads_sample=2, iters=3):
         "kind": "port",
         "sample": (f"config 4 forward+backward on {heads_sample} of {cfg.heads} heads (all "
                    f"{len(cfg.lengths)} sequences, {n} tokens), fp32 numpy einsum as in the "
-                   f"reference's numpy branch; median of {iters} after 1 warmup; "
-                   f"{sec * 1e3:.0f} ms per sample step; host os.cpu_count()={os.cpu_count()}, "
-                   f"affinity={len(os.sched_getaffinity(0))}"),
+                   f"reference's numpy branch (backward: closed-form restatement); median of "
+                   f"{iters} after {warmup} warmup; {sec * 1e3:.0f} ms per sample step; host "
+                   f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}; "
+                   "einsum without optimize is single-threaded"),
     }
+
+
+def cpu_plumbing():
+    """Config 1 on the CPU oracle (the reference's own CPU case), plus a config 2 RMSNorm sample."""
+    import numpy as np
+
+    from oracle.attention import attention_fwd
+    from oracle.norms import rmsnorm_fwd
+    from scree_amd import workloads
+
+    lengths = workloads.config1_lengths()
+    n = int(sum(lengths))
+    off = np.zeros(len(lengths) + 1, dtype=np.int32)
+    off[1:] = np.cumsum(lengths)
+    rng = np.random.default_rng(0)
+    q, k, v = (rng.standard_normal((n, 4, 32)).astype(np.float32) for _ in range(3))
+    out = {"cfg1_tokens": n}
+    for causal in (False, True):
+        sec = _cpu_median(lambda: attention_fwd(q, k, v, off, causal=causal, dtype=np.float32,
+                                                impl="einsum"))
+        out[f"cfg1_attn_causal_{causal}_ms"] = round(sec * 1e3, 3)
+    x128 = rng.standard_normal((n, 128)).astype(np.float32)
+    sec = _cpu_median(lambda: rmsnorm_fwd(x128, None, 1e-6, dtype=np.float32))
+    out["cfg1_rmsnorm_1980x128_ms"] = round(sec * 1e3, 3)
+    cfg2 = workloads.config2()
+    rows = 2048  # row sample of config 2 (19758 x 4096), fp32 numpy
+    xs = rng.standard_normal((rows, cfg2.hidden)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(cfg2.hidden)).astype(np.float32)
+    sec = _cpu_median(lambda: rmsnorm_fwd(xs, w, cfg2.eps, dtype=np.float32))
+    out["cfg2_rmsnorm_fwd_cpu_GBps"] = round(workloads.norm_fwd_bytes(rows, cfg2.hidden, 4, False)
+                                             / sec / 1e9, 2)
+    out["cfg2_rmsnorm_fwd_cpu_sample"] = f"{rows} of {cfg2.total} rows, fp32, 1 core"
+    return out
 
 
 def load_traffic(kernel: str, workload: str):
@@ -246,8 +286,8 @@ def load_traffic(kernel: str, workload: str):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary configs")
     args = ap.parse_args()
@@ -325,6 +365,8 @@ def main() -> int:
         log("cpu baseline ...")
         cpu = cpu_baseline(cfg4)
         log(f"cpu: {cpu['value'] * 1e3:.3f} GFLOP/s")
+        secondary["cpu_plumbing"] = cpu_plumbing()
+        log(f"cpu plumbing: {secondary['cpu_plumbing']}")
 
     line = {
         "metric": "causal varlen attn fwd & fwd+bwd TFLOP/s, MFMA %; varlen RMSNorm HBM GB/s",

@@ -209,48 +209,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
-__device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
-}
-
-// A ROWS x D tile of one head, staged row-major through registers into LDS.
-// Loads go through a buffer descriptor that covers only the rows below
-// `limit`, so rows past the sequence end read as zeros and nothing outside
-// it is touched; the per-thread byte offsets are fixed and computed once.
-template <typename T, int D, int ROWS>
-struct Stage {
-  static constexpr int CPR = D / 8;  // 16-byte chunks per row
-  static constexpr int UNITS = ROWS * CPR;
-  static_assert(UNITS % kThreads == 0, "tile must split evenly over the block");
-  static constexpr int CH = UNITS / kThreads;
-  uint32_t off[CH];
-  uint4 r[CH];
-
-  __device__ __forceinline__ void init(int64_t row_stride) {
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int u = j * kThreads + threadIdx.x;
-      off[j] = (uint32_t)(((int64_t)(u / CPR) * row_stride + (u % CPR) * 8) * (int64_t)sizeof(T));
-    }
-  }
-  // rows [row0, row0 + ROWS) of a sequence starting at `base`; rows >= limit read as 0
-  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t row_stride, int row0,
-                                       int limit) {
-    const int valid = min(ROWS, limit - row0);
-    const uint32_t bytes = valid > 0 ? (uint32_t)((int64_t)valid * row_stride * (int64_t)sizeof(T)) : 0u;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)row0 * row_stride, bytes);
-#pragma unroll
-    for (int j = 0; j < CH; ++j) r[j] = buf_ld16(rs, off[j]);
-  }
-  // lds[row][col], leading dimension ld (elements)
-  __device__ __forceinline__ void put_rows(T* lds, int ld) const {
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int u = j * kThreads + threadIdx.x;
-      st16(lds + (u / CPR) * ld + (u % CPR) * 8, r[j]);
-    }
-  }
-};
 
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 lds_frag16(const T* p) {
@@ -259,13 +217,11 @@ __device__ __forceinline__ typename VecT<T>::x8 lds_frag16(const T* p) {
 // Transposed operand from a row-major LDS tile X[row][col] (leading dim ld).
 // ds_read_tr16_b64 hands lane 16G + i, slot j, element i%4 of the 8 bytes
 // addressed by lane 16G + 4j + i/4.  With each lane addressing
-// X[4g + (lr%16)/4][16*(lr/16) + 4*(lr%4)] (tr_lane_offset), lane (lr, g)
-// receives X[4g + j][lr] in slots j = 0..3; a second read 8 rows further
-// gives slots 4..7.  That is the k-run layout {4g + 0..3, 8 + 4g + 0..3} of
-// the MFMA operands here (rows of X are the k axis, columns the M axis).
-__device__ __forceinline__ int tr_lane_offset(int lr, int g, int ld) {
-  return (4 * g + ((lr & 15) >> 2)) * ld + 16 * (lr >> 4) + 4 * (lr & 3);
-}
+// X[4g + (lr%16)/4][16*(lr/16) + 4*(lr%4)] (swz_tr_off adds the tile
+// swizzle), lane (lr, g) receives X[4g + j][lr] in slots j = 0..3; a second
+// read 8 rows further gives slots 4..7.  That is the k-run layout
+// {4g + 0..3, 8 + 4g + 0..3} of the MFMA operands here (rows of X are the k
+// axis, columns the M axis).
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 lds_frag_tr(const T* p, int ld) {
   typedef short s4 __attribute__((ext_vector_type(4)));
@@ -430,7 +386,35 @@ __device__ __forceinline__ int swz_tr_off(int lr, int g, int dt) {
   return r * D + ((c ^ swz<D>(r)) << 3) + 4 * (lr & 1);
 }
 
-// Per-wave state of the forward loop over 64-key blocks.
+// Reductions across the two 32-lane halves of a wave: v_permlane32_swap
+// exchanges the upper 32 lanes of its first register with the lower 32 lanes
+// of its second, so starting from two copies of x every lane ends up holding
+// x[l % 32] and x[32 + l % 32] (no LDS round trip).  Emitted directly: the
+// compiler's builtin folds the two results into one when both inputs are the
+// same value.  The s_nop covers the VALU-write -> permlane read hazard.
+__device__ __forceinline__ void half_pair(float x, float& a, float& b) {
+  float lo = x, hi = x;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+  a = lo;
+  b = hi;
+}
+__device__ __forceinline__ float halves_max(float x) {
+  float a, b;
+  half_pair(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  float a, b;
+  half_pair(x, a, b);
+  return a + b;
+}
+
+// Running max starts finite: the first tile always rescales (by exp2 of a
+// huge negative number, i.e. 0), and no -inf special case is needed.
+constexpr float kMaxInit = -1e30f;
+
+// Per-wave state of the forward loop over 64-key blocks.  The workgroup's
+// 4 waves hold the item's 128 queries (32 per wave) and share the K/V tiles.
 template <typename T, int D>
 struct FwdState {
   typedef typename VecT<T>::x8 x8;
@@ -438,7 +422,7 @@ struct FwdState {
   int koff[D / 16];         // swizzled K row-read offsets
   int voffs[D / 32];        // swizzled V transposed-read offsets
   f32x16 oacc[D / 32];      // O^T accumulators
-  float m_run, l_run;       // running max (raw scores) and row sum
+  float m_run, l_run;       // running max (raw scores) and row sum (this lane's keys)
   DmaTile<T, D, kBN> dK, dV;
   const T* kh;
   const T* vh;
@@ -447,9 +431,9 @@ struct FwdState {
   float scale_log2, rescale_gap;
 };
 
-// One 64-key block: start the DMA of block kb+1 into `nxt`, then compute on
-// `cur` (K tile, then V tile). The restrict qualifiers tell the compiler the
-// two buffers are disjoint, so it keeps the DMA in flight across the reads.
+// One 64-key block kb: start the DMA of block kb + 1 into `nxt`, then compute
+// on `cur` (K tile, then V tile).  The restrict qualifiers tell the compiler
+// the two buffers are disjoint, so it keeps the DMA in flight across the reads.
 template <typename T, int D, bool CAUSAL>
 __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* __restrict__ cur,
                                           T* __restrict__ nxt) {
@@ -488,7 +472,7 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
     float mx = sacc[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = halves_max(mx);
     const bool grow = mx > st.m_run + st.rescale_gap;
     if (__any(grow)) {
       const float m_new = grow ? mx : st.m_run;
@@ -500,13 +484,14 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
         for (int i = 0; i < 16; ++i) st.oacc[dt][i] *= alpha;
       st.m_run = m_new;
     }
-    const float mb = st.m_run == kNegInf ? 0.f : st.m_run * st.scale_log2;
+    const float mb = st.m_run * st.scale_log2;
+    float ls[2] = {st.l_run, 0.f};  // the row sum in fp32, of the unrounded weights
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = fast_exp2(fmaf(sacc[i], st.scale_log2, -mb));
-      sacc[i] = p;
-      st.l_run += p;
+      sacc[i] = fast_exp2(fmaf(sacc[i], st.scale_log2, -mb));
+      ls[i & 1] += sacc[i];
     }
+    st.l_run = ls[0] + ls[1];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const x8 pf = pack_frag<T>(sacc, 8 * hh);
@@ -516,7 +501,7 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
                              st.oacc[dt]);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block kb+1 has landed
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block kb + 1 has landed
   __syncthreads();
 }
 
@@ -527,10 +512,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     int tmax, int head_major, int heads, Strides sq, Strides sk, Strides sv, Strides so,
     float scale, float scale_log2) {
   constexpr int TILE = kBN * D;  // elements per K or V tile
-  // Two distinct arrays (K then V in each), alternated at compile-time
-  // positions of the loop below.
-  __shared__ __align__(16) T bufA[2 * TILE];
-  __shared__ __align__(16) T bufB[2 * TILE];
+  constexpr int BUF = 2 * TILE;  // one buffer: K tile then V tile
+  __shared__ __align__(16) T smem[2 * BUF];
 
   int item, h;
   if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
@@ -553,6 +536,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   st.nkb = (kend_wg + kBN - 1) / kBN;
   st.kend_wave = wave_live ? (CAUSAL ? min(L, st.qw0 + 32) : L) : 0;
 
+  T* bufA = smem;
+  T* bufB = smem + BUF;
   st.dK.init(sk.row, st.wave, lane);
   st.dV.init(sv.row, st.wave, lane);
   st.dK.load(bufA, st.kh, sk.row, 0, L, st.wave);
@@ -562,6 +547,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const T* qrow = q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
+    // Materialize the fragments before the barrier (the compiler would sink
+    // the loads into the block loop, whose counter waits would then also wait
+    // out the freshly issued DMA).
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.qf[s]));
   }
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) st.koff[s] = swz_off<D>(st.lr, 2 * s + st.g);
@@ -571,26 +561,24 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   st.rescale_gap = kRescaleLog2Gap / scale_log2;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) st.oacc[dt] = zero16();
-  st.m_run = kNegInf;
+  st.m_run = kMaxInit;
   st.l_run = 0.f;
 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // Unrolled by two so that each call sees its buffers at fixed positions.
   for (int kb = 0; kb < st.nkb; kb += 2) {
     fwd_block<T, D, CAUSAL>(st, kb, bufA, bufB);
     if (kb + 1 < st.nkb) fwd_block<T, D, CAUSAL>(st, kb + 1, bufB, bufA);
   }
-  const int g = st.g, lr = st.lr;
-  const float m_run = st.m_run, l_run = st.l_run;
-  const f32x16* oacc = st.oacc;
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   if (wave_live && my_q < L) {
+    const float l_tot = halves_sum(st.l_run);
     const float inv_l = 1.0f / l_tot;
     T* orow = o + (int64_t)(start + my_q) * so.row + (int64_t)h * so.head;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) store_row_slice<T>(orow, 32 * dt, g, oacc[dt], inv_l);
-    if (g == 0) lse[(int64_t)(start + my_q) * heads + h] = m_run * scale + logf(l_tot);
+    for (int dt = 0; dt < D / 32; ++dt)
+      store_row_slice<T>(orow, 32 * dt, st.g, st.oacc[dt], inv_l);
+    if (st.g == 0) lse[(int64_t)(start + my_q) * heads + h] = st.m_run * scale + logf(l_tot);
   }
 }
 
@@ -598,13 +586,68 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
 // Per item: 128 queries (32 per wave) loop over 64-key blocks.
 //   S^T = K Q^T, dP^T = V dO^T (Q, dO operands in registers; K, V from LDS)
 //   P^T = exp(S^T - LSE), dS^T = P^T (dP^T - Delta)
-//   dQ^T += K^T dS^T (K^T read transposed from the row-major K tile; dS^T in registers)
+//   dQ^T += K^T dS^T (K^T read transposed from the K tile; dS^T in registers)
+// K and V tiles arrive by DMA into swizzled LDS tiles, as in the forward.
 // Delta = rowsum(O * dO) is computed here from the stored O and written out
 // for the dK/dV pass.  Keys past L hold zeros in K and V, so their dS^T
 // multiplies a zero row of K^T: no length mask is needed.
 template <typename T, int D>
-constexpr int dq_buffers() {
-  return 2;
+struct DqState {
+  typedef typename VecT<T>::x8 x8;
+  x8 qf[D / 16], df[D / 16];  // this lane's Q and dO rows, MFMA B fragments
+  int koff[D / 16];           // swizzled row-read offsets (K and V tiles)
+  int ktr[D / 32];            // swizzled transposed-read offsets (K^T)
+  f32x16 dqacc[D / 32];       // dQ^T accumulators
+  f32x16 neg_delta;           // dP^T accumulates onto -Delta: it comes out as dP^T - Delta
+  float lse2;                 // this lane's LSE * log2(e)
+  DmaTile<T, D, kBN> dK, dV;
+  const T* kh;
+  const T* vh;
+  int64_t krow, vrow;
+  int L, nkb, kend_wave, qw0, wave, lr, g;
+  float scale_log2;
+};
+
+// One 64-key block kb (see fwd_block for the buffer discipline).
+template <typename T, int D, bool CAUSAL>
+__device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __restrict__ cur,
+                                         T* __restrict__ nxt) {
+  typedef typename VecT<T>::x8 x8;
+  constexpr int TILE = kBN * D;
+  const T* sK = cur;
+  const T* sV = cur + TILE;
+  if (kb + 1 < st.nkb) {
+    st.dK.load(nxt, st.kh, st.krow, (kb + 1) * kBN, st.L, st.wave);
+    st.dV.load(nxt + TILE, st.vh, st.vrow, (kb + 1) * kBN, st.L, st.wave);
+  }
+  const int kbase = kb * kBN;
+  const int nt = kbase < st.kend_wave ? (kbase + 32 < st.kend_wave ? 2 : 1) : 0;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (t >= nt) break;
+    f32x16 sacc = zero16(), pacc = st.neg_delta;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      sacc = mfma32(lds_frag16(sK + 32 * t * D + st.koff[s]), st.qf[s], sacc);
+      pacc = mfma32(lds_frag16(sV + 32 * t * D + st.koff[s]), st.df[s], pacc);
+    }
+    if (CAUSAL && kbase + 32 * t == st.qw0) mask_rows_above(sacc, st.lr - 4 * st.g);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = fast_exp2(fmaf(sacc[i], st.scale_log2, -st.lse2));
+      sacc[i] = p * pacc[i];  // dS^T = P^T (dP^T - Delta)
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const x8 sf = pack_frag<T>(sacc, 8 * hh);
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+        st.dqacc[dt] = mfma32(lds_frag_tr(sK + (32 * t + 16 * hh) * D + st.ktr[dt], D), sf,
+                              st.dqacc[dt]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block kb + 1 has landed
+  __syncthreads();
 }
 
 template <typename T, int D, bool CAUSAL>
@@ -612,109 +655,83 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
     float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
-    Strides so, Strides sdq, float scale, float scale_log2) {
-  constexpr int NBUF = dq_buffers<T, D>();
-  constexpr int KLD = D + 8;
-  constexpr int BUF = 2 * kBN * KLD;  // K rows, V rows
-  __shared__ __align__(16) T smem[NBUF * BUF];
+    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq,
+    Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2) {
+  typedef typename VecT<T>::x8 x8;
+  constexpr int TILE = kBN * D;
+  constexpr int BUF = 2 * TILE;  // K tile then V tile
+  __shared__ __align__(16) T smem[2 * BUF];
 
   int item, h;
   if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
   const int4 it = items[item];
   const int start = it.z, L = it.w, q0 = it.y * kBM;
-  const int wave = wave_id(), lane = threadIdx.x & (kWave - 1);
-  const int g = lane >> 5, lr = lane & 31;
-  const int qw0 = q0 + 32 * wave;
-  const int my_q = qw0 + lr;
-  const bool wave_live = qw0 < L;
-  const bool row_ok = my_q < L;
+  DqState<T, D> st;
+  st.wave = wave_id();
+  const int lane = threadIdx.x & (kWave - 1);
+  st.g = lane >> 5;
+  st.lr = lane & 31;
+  st.qw0 = q0 + 32 * st.wave;
+  const int my_q = st.qw0 + st.lr;
+  const bool wave_live = st.qw0 < L;
+  st.L = L;
+  st.kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
+  st.vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
+  st.krow = sk.row;
+  st.vrow = sv.row;
+  const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
+  st.nkb = (kend_wg + kBN - 1) / kBN;
+  st.kend_wave = wave_live ? (CAUSAL ? min(L, st.qw0 + 32) : L) : 0;
 
-  typedef typename VecT<T>::x8 x8;
-  x8 qf[D / 16], df[D / 16];
+  T* bufA = smem;
+  T* bufB = smem + BUF;
+  st.dK.init(sk.row, st.wave, lane);
+  st.dV.init(sv.row, st.wave, lane);
+  st.dK.load(bufA, st.kh, sk.row, 0, L, st.wave);
+  st.dV.load(bufA + TILE, st.vh, sv.row, 0, L, st.wave);
+
   float dl = 0.f;
-  {
+  {  // rows past L read row L-1: their results are never stored
     const int64_t tok = start + min(my_q, L - 1);
     const T* qrow = q + tok * sq.row + (int64_t)h * sq.head;
     const T* drow = dout + tok * sdo.row + (int64_t)h * sdo.head;
     const T* orow = o + tok * so.row + (int64_t)h * so.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
-      qf[s] = gmem_frag16(qrow + 16 * s + 8 * g);
-      df[s] = gmem_frag16(drow + 16 * s + 8 * g);
-      const x8 of = gmem_frag16(orow + 16 * s + 8 * g);
+      st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
+      st.df[s] = gmem_frag16(drow + 16 * s + 8 * st.g);
+      const x8 of = gmem_frag16(orow + 16 * s + 8 * st.g);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)df[s][j];
+      for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)st.df[s][j];
     }
-  }
-  dl += __shfl_xor(dl, 32, kWave);
-  const float lse2 = lse[(int64_t)(start + min(my_q, L - 1)) * heads + h] * kLog2e;
-  if (row_ok && g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
-
-  const T* kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
-  const T* vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
-  const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
-  const int nkb = (kend_wg + kBN - 1) / kBN;
-  const int kend_wave = wave_live ? (CAUSAL ? min(L, qw0 + 32) : L) : 0;
-
-  f32x16 dqacc[D / 32];
+    st.lse2 = lse[tok * heads + h] * kLog2e;
+    // Materialize the fragments before the barrier (see the forward).
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) dqacc[dt] = zero16();
+    for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.qf[s]), "+v"(st.df[s]));
+  }
+  dl = halves_sum(dl);
+  if (my_q < L && st.g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) st.neg_delta[i] = -dl;
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) st.koff[s] = swz_off<D>(st.lr, 2 * s + st.g);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) st.ktr[dt] = swz_tr_off<D>(st.lr, st.g, dt);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) st.dqacc[dt] = zero16();
+  st.scale_log2 = scale_log2;
 
-  Stage<T, D, kBN> stK, stV;
-  stK.init(sk.row);
-  stV.init(sv.row);
-  stK.load(kh, sk.row, 0, L);
-  stV.load(vh, sv.row, 0, L);
-  stK.put_rows(smem, KLD);
-  stV.put_rows(smem + kBN * KLD, KLD);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int ktr = tr_lane_offset(lr, g, KLD);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const T* sK = smem + (NBUF == 2 ? (kb & 1) : 0) * BUF;
-    const T* sV = sK + kBN * KLD;
-    if (kb + 1 < nkb) {
-      stK.load(kh, sk.row, (kb + 1) * kBN, L);
-      stV.load(vh, sv.row, (kb + 1) * kBN, L);
-    }
-    const int kbase = kb * kBN;
-    const int nt = kbase < kend_wave ? (kbase + 32 < kend_wave ? 2 : 1) : 0;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (t >= nt) continue;
-      f32x16 sacc = zero16(), pacc = zero16();
-#pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
-        sacc = mfma32(lds_frag16(sK + (32 * t + lr) * KLD + 16 * s + 8 * g), qf[s], sacc);
-        pacc = mfma32(lds_frag16(sV + (32 * t + lr) * KLD + 16 * s + 8 * g), df[s], pacc);
-      }
-      if (CAUSAL && kbase + 32 * t == qw0) mask_rows_above(sacc, lr - 4 * g);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = fast_exp2(fmaf(sacc[i], scale_log2, -lse2));
-        sacc[i] = p * (pacc[i] - dl);  // dS^T
-      }
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const x8 sf = pack_frag<T>(sacc, 8 * hh);
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-          dqacc[dt] = mfma32(lds_frag_tr(sK + ktr + (32 * t + 16 * hh) * KLD + 32 * dt, KLD), sf,
-                             dqacc[dt]);
-      }
-    }
-    if (kb + 1 < nkb) {
-      if (NBUF == 1) __syncthreads();
-      T* nK = smem + (NBUF == 2 ? ((kb + 1) & 1) : 0) * BUF;
-      stK.put_rows(nK, KLD);
-      stV.put_rows(nK + kBN * KLD, KLD);
-    }
-    __syncthreads();
+  // Unrolled by two so that each call sees its buffers at fixed positions.
+  for (int kb = 0; kb < st.nkb; kb += 2) {
+    dq_block<T, D, CAUSAL>(st, kb, bufA, bufB);
+    if (kb + 1 < st.nkb) dq_block<T, D, CAUSAL>(st, kb + 1, bufB, bufA);
   }
-  if (wave_live && row_ok) {
+  if (wave_live && my_q < L) {
     T* out = dq + (int64_t)(start + my_q) * sdq.row + (int64_t)h * sdq.head;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) store_row_slice<T>(out, 32 * dt, g, dqacc[dt], scale);
+    for (int dt = 0; dt < D / 32; ++dt) store_row_slice<T>(out, 32 * dt, st.g, st.dqacc[dt], scale);
   }
 }
 
@@ -722,25 +739,159 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
 // Per item: 128 keys (32 per wave) loop over blocks of BQ queries.
 //   S = Q K^T, dP = dO V^T (K, V operands in registers; Q, dO from LDS)
 //   P = exp(S - LSE), dS = P (dP - Delta)
-//   dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T read transposed from the row-major
-//   LDS tiles; P, dS in registers)
-// Queries past L hold zeros in Q and dO (and LSE = Delta = 0), so they add
-// nothing to dK or dV: no length mask is needed.
-// D = 128 holds K, V, dK and dV for its keys in registers and needs the full
-// register file (one wave per SIMD); smaller D fits two.
+//   dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T read transposed from the LDS
+//   tiles; P, dS in registers)
+// Q and dO tiles arrive by DMA into swizzled LDS tiles, as in the forward;
+// each block's LSE and -Delta rows are staged beside them.  Queries past L
+// hold zeros in Q and dO (and LSE = Delta = 0), so they add nothing to dK or
+// dV: no length mask is needed.  D = 128 holds K, V, dK and dV for its keys
+// in registers and needs the full register file (one wave per SIMD).
+template <int D>
+constexpr int dkv_bq() {
+  return D >= 128 ? 32 : 64;
+}
+
+template <typename T, int D>
+struct DkvState {
+  typedef typename VecT<T>::x8 x8;
+  static constexpr int BQ = dkv_bq<D>();
+  x8 kf[D / 16], vf[D / 16];      // this lane's K and V rows, MFMA B fragments
+  f32x16 dkacc[D / 32], dvacc[D / 32];
+  int qoff[D / 16];               // swizzled row-read offsets (Q and dO tiles)
+  int qtr[D / 32];                // swizzled transposed-read offsets
+  DmaTile<T, D, BQ> dQ, dO;
+  const T* qh;
+  const T* dh;
+  const float* lse_h;             // lse / delta of this head at the sequence start
+  const float* delta_h;
+  int64_t qrow, drow;
+  int heads, L, qbeg, nqb, kw0, wave, lr, g;
+  bool wave_live;
+  float pl, pd;                   // staged LSE and Delta of one query row
+  float scale_log2;
+};
+
+// LSE and Delta of query row `qq` into registers (threads < BQ own one row
+// each); they are converted only when stored, so the loads stay in flight.
+template <typename T, int D>
+__device__ __forceinline__ void dkv_load_rows(DkvState<T, D>& st, int qq) {
+  const int64_t idx = (int64_t)min(qq, st.L - 1) * st.heads;
+  st.pl = qq < st.L ? st.lse_h[idx] : 0.f;
+  st.pd = qq < st.L ? st.delta_h[idx] : 0.f;
+}
+__device__ __forceinline__ void dkv_store_rows(float* rows, int bq, float pl, float pd) {
+  rows[threadIdx.x] = pl * kLog2e;
+  rows[bq + threadIdx.x] = -pd;
+}
+
+// One block b of BQ queries (see fwd_block for the buffer discipline).
+// `lcur` holds [LSE*log2(e) | -Delta] of the block's rows.
+template <typename T, int D, bool CAUSAL>
+__device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __restrict__ cur,
+                                          T* __restrict__ nxt, const float* __restrict__ lcur) {
+  typedef typename VecT<T>::x8 x8;
+  constexpr int BQ = DkvState<T, D>::BQ;
+  constexpr int NQT = BQ / 32;
+  constexpr int TILE = BQ * D;
+  const T* sQ = cur;
+  const T* sO = cur + TILE;
+  const int qb = st.qbeg + b * BQ;
+  if (b + 1 < st.nqb) {
+    st.dQ.load(nxt, st.qh, st.qrow, qb + BQ, st.L, st.wave);
+    st.dO.load(nxt + TILE, st.dh, st.drow, qb + BQ, st.L, st.wave);
+  }
+  if (st.wave_live) {
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+      const int qt0 = qb + 32 * u;
+      if (qt0 >= st.L) continue;
+      if (CAUSAL && qt0 < st.kw0) continue;  // every query of the tile precedes every key
+      // lane: key (column); element i: query qt0 + acc_row0(i) + 4g (row).
+      // dP accumulates onto -Delta of its row, so it comes out as dP - Delta.
+      f32x16 sacc = zero16(), pacc;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const float4 d4 = *reinterpret_cast<const float4*>(lcur + BQ + 32 * u + 8 * i4 + 4 * st.g);
+        pacc[4 * i4 + 0] = d4.x;
+        pacc[4 * i4 + 1] = d4.y;
+        pacc[4 * i4 + 2] = d4.z;
+        pacc[4 * i4 + 3] = d4.w;
+      }
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) {
+        sacc = mfma32(lds_frag16(sQ + 32 * u * D + st.qoff[s]), st.kf[s], sacc);
+        pacc = mfma32(lds_frag16(sO + 32 * u * D + st.qoff[s]), st.vf[s], pacc);
+      }
+      f32x16 pv;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const float4 l4 = *reinterpret_cast<const float4*>(lcur + 32 * u + 8 * i4 + 4 * st.g);
+        const float la[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * i4 + e;
+          const float p = fast_exp2(fmaf(sacc[i], st.scale_log2, -la[e]));
+          pv[i] = p;
+          sacc[i] = p * pacc[i];  // dS = P (dP - Delta)
+        }
+      }
+      if (CAUSAL && qt0 == st.kw0) {
+        // diagonal tile: queries before the key contribute nothing
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (acc_row0(i) < st.lr - 4 * st.g) {
+            pv[i] = 0.f;
+            sacc[i] = 0.f;
+          }
+        }
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const x8 pf = pack_frag<T>(pv, 8 * hh);
+        const x8 sf = pack_frag<T>(sacc, 8 * hh);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          st.dvacc[dt] = mfma32(lds_frag_tr(sO + (32 * u + 16 * hh) * D + st.qtr[dt], D), pf,
+                                st.dvacc[dt]);
+          st.dkacc[dt] = mfma32(lds_frag_tr(sQ + (32 * u + 16 * hh) * D + st.qtr[dt], D), sf,
+                                st.dkacc[dt]);
+        }
+      }
+    }
+  }
+}
+
+// Block b with the row staging around it: the next block's LSE / Delta rows
+// load during the block and land in `lnxt` before the closing barrier.
+template <typename T, int D, bool CAUSAL>
+__device__ __forceinline__ void dkv_step(DkvState<T, D>& st, int b, const T* cur, T* nxt,
+                                         const float* lcur, float* lnxt) {
+  constexpr int BQ = DkvState<T, D>::BQ;
+  const bool more = b + 1 < st.nqb;
+  if (more && threadIdx.x < BQ) dkv_load_rows(st, st.qbeg + (b + 1) * BQ + (int)threadIdx.x);
+  dkv_block<T, D, CAUSAL>(st, b, cur, nxt, lcur);
+  if (more && threadIdx.x < BQ) dkv_store_rows(lnxt, BQ, st.pl, st.pd);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block b + 1 has landed
+  __syncthreads();
+}
+
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
     T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq, Strides sk, Strides sv,
-    Strides sdk, Strides sdv, float scale, float scale_log2) {
-  constexpr int BQ = D >= 128 ? 32 : 64;
-  constexpr int NQT = BQ / 32;
-  constexpr int LD = D + 8;
-  constexpr int BUF = 2 * BQ * LD;  // Q rows, dO rows
-  __shared__ __align__(16) T smem[2 * BUF];
-  __shared__ __align__(16) float sLD[2][2][BQ];  // [buffer][lse*log2e | delta][row]
+    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq,
+    Strides sk, Strides sv, Strides sdk, Strides sdv, float scale, float scale_log2) {
+  constexpr int BQ = dkv_bq<D>();
+  constexpr int TILE = BQ * D;
+  constexpr int BUF = 2 * TILE;  // Q tile then dO tile
+  // Two [Q tile | dO tile] buffers, then two [LSE*log2(e) rows | -Delta rows]
+  // buffers.  One LDS object: with several, the compiler's LDS lowering drops
+  // the alias scopes that keep the DMA and the tile reads apart.
+  constexpr int ROWS_T = 2 * BQ * (int)(sizeof(float) / sizeof(T));  // one row buffer, in T
+  __shared__ __align__(16) T smem[2 * BUF + 2 * ROWS_T];
+  float* sLD0 = reinterpret_cast<float*>(smem + 2 * BUF);
+  float* sLD1 = reinterpret_cast<float*>(smem + 2 * BUF + ROWS_T);
 
   int item, h;
   if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
@@ -748,136 +899,75 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
   const int start = it.z, L = it.w;
   const int nblk = (L + kBM - 1) / kBM;
   const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
-  const int wave = wave_id(), lane = threadIdx.x & (kWave - 1);
-  const int g = lane >> 5, lr = lane & 31;
-  const int kw0 = k0 + 32 * wave;
-  const int my_k = kw0 + lr;
-  const bool wave_live = kw0 < L;
-  const bool key_ok = my_k < L;
+  DkvState<T, D> st;
+  st.wave = wave_id();
+  const int lane = threadIdx.x & (kWave - 1);
+  st.g = lane >> 5;
+  st.lr = lane & 31;
+  st.kw0 = k0 + 32 * st.wave;
+  const int my_k = st.kw0 + st.lr;
+  st.wave_live = st.kw0 < L;
+  st.L = L;
+  st.heads = heads;
+  st.qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
+  st.dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
+  st.qrow = sq.row;
+  st.drow = sdo.row;
+  st.lse_h = lse + (int64_t)start * heads + h;
+  st.delta_h = delta + (int64_t)start * heads + h;
+  st.qbeg = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
+  st.nqb = (L - st.qbeg + BQ - 1) / BQ;
+  st.scale_log2 = scale_log2;
 
-  typedef typename VecT<T>::x8 x8;
-  x8 kf[D / 16], vf[D / 16];
-  {
+  T* bufA = smem;
+  T* bufB = smem + BUF;
+  st.dQ.init(sq.row, st.wave, lane);
+  st.dO.init(sdo.row, st.wave, lane);
+  st.dQ.load(bufA, st.qh, sq.row, st.qbeg, L, st.wave);
+  st.dO.load(bufA + TILE, st.dh, sdo.row, st.qbeg, L, st.wave);
+  if (threadIdx.x < BQ) {
+    dkv_load_rows(st, st.qbeg + (int)threadIdx.x);
+    dkv_store_rows(sLD0, BQ, st.pl, st.pd);
+  }
+  {  // keys past L read row L-1: their results are never stored
     const int64_t tok = start + min(my_k, L - 1);
     const T* krow = k + tok * sk.row + (int64_t)h * sk.head;
     const T* vrow = v + tok * sv.row + (int64_t)h * sv.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
-      kf[s] = gmem_frag16(krow + 16 * s + 8 * g);
-      vf[s] = gmem_frag16(vrow + 16 * s + 8 * g);
+      st.kf[s] = gmem_frag16(krow + 16 * s + 8 * st.g);
+      st.vf[s] = gmem_frag16(vrow + 16 * s + 8 * st.g);
     }
+    // Materialize the fragments here, before the barrier: left to itself the
+    // compiler sinks these loads into the block loop, where their counter
+    // waits then also wait out each block's freshly issued DMA.
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.kf[s]), "+v"(st.vf[s]));
   }
-  f32x16 dkacc[D / 32], dvacc[D / 32];
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) st.qoff[s] = swz_off<D>(st.lr, 2 * s + st.g);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) st.qtr[dt] = swz_tr_off<D>(st.lr, st.g, dt);
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) {
-    dkacc[dt] = zero16();
-    dvacc[dt] = zero16();
+    st.dkacc[dt] = zero16();
+    st.dvacc[dt] = zero16();
   }
 
-  const T* qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
-  const T* dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
-  const int qbeg = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
-  const int nqb = L > qbeg ? (L - qbeg + BQ - 1) / BQ : 0;
-
-  Stage<T, D, BQ> stQ, stO;
-  stQ.init(sq.row);
-  stO.init(sdo.row);
-  float pl = 0.f, pd = 0.f;
-  auto load_block = [&](int qb) {
-    stQ.load(qh, sq.row, qb, L);
-    stO.load(dh, sdo.row, qb, L);
-    if (threadIdx.x < BQ) {
-      const int qq = qb + threadIdx.x;
-      const int64_t idx = (int64_t)(start + min(qq, L - 1)) * heads + h;
-      pl = qq < L ? lse[idx] * kLog2e : 0.f;
-      pd = qq < L ? delta[idx] : 0.f;
-    }
-  };
-  auto put_block = [&](int buf) {
-    T* b = smem + buf * BUF;
-    stQ.put_rows(b, LD);
-    stO.put_rows(b + BQ * LD, LD);
-    if (threadIdx.x < BQ) {
-      sLD[buf][0][threadIdx.x] = pl;
-      sLD[buf][1][threadIdx.x] = pd;
-    }
-  };
-  if (nqb > 0) {
-    load_block(qbeg);
-    put_block(0);
-  }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int qtr = tr_lane_offset(lr, g, LD);
-  for (int b = 0; b < nqb; ++b) {
-    const int qb = qbeg + b * BQ;
-    const T* sQ = smem + (b & 1) * BUF;
-    const T* sO = sQ + BQ * LD;
-    const float* sL = sLD[b & 1][0];
-    const float* sDl = sLD[b & 1][1];
-    if (b + 1 < nqb) load_block(qb + BQ);
-    if (wave_live) {
-#pragma unroll
-      for (int u = 0; u < NQT; ++u) {
-        const int qt0 = qb + 32 * u;
-        if (qt0 >= L) continue;
-        if (CAUSAL && qt0 < kw0) continue;  // every query of the tile precedes every key
-        f32x16 sacc = zero16(), pacc = zero16();
-#pragma unroll
-        for (int s = 0; s < D / 16; ++s) {
-          sacc = mfma32(lds_frag16(sQ + (32 * u + lr) * LD + 16 * s + 8 * g), kf[s], sacc);
-          pacc = mfma32(lds_frag16(sO + (32 * u + lr) * LD + 16 * s + 8 * g), vf[s], pacc);
-        }
-        // lane: key my_k (column); element i: query qt0 + acc_row0(i) + 4g (row)
-        f32x16 pv;
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int r0 = 32 * u + 8 * i4 + 4 * g;
-          const float4 l4 = *reinterpret_cast<const float4*>(sL + r0);
-          const float4 d4 = *reinterpret_cast<const float4*>(sDl + r0);
-          const float la[4] = {l4.x, l4.y, l4.z, l4.w};
-          const float da[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = 4 * i4 + e;
-            const float p = fast_exp2(fmaf(sacc[i], scale_log2, -la[e]));
-            pv[i] = p;
-            sacc[i] = p * (pacc[i] - da[e]);  // dS
-          }
-        }
-        if (CAUSAL && qt0 == kw0) {
-          // diagonal tile: queries before the key contribute nothing
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            if (acc_row0(i) < lr - 4 * g) {
-              pv[i] = 0.f;
-              sacc[i] = 0.f;
-            }
-          }
-        }
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const x8 pf = pack_frag<T>(pv, 8 * hh);
-          const x8 sf = pack_frag<T>(sacc, 8 * hh);
-#pragma unroll
-          for (int dt = 0; dt < D / 32; ++dt) {
-            dvacc[dt] = mfma32(lds_frag_tr(sO + qtr + (32 * u + 16 * hh) * LD + 32 * dt, LD), pf,
-                               dvacc[dt]);
-            dkacc[dt] = mfma32(lds_frag_tr(sQ + qtr + (32 * u + 16 * hh) * LD + 32 * dt, LD), sf,
-                               dkacc[dt]);
-          }
-        }
-      }
-    }
-    if (b + 1 < nqb) put_block((b + 1) & 1);
-    __syncthreads();
+  // Unrolled by two so that each call sees its buffers at fixed positions.
+  for (int b = 0; b < st.nqb; b += 2) {
+    dkv_step<T, D, CAUSAL>(st, b, bufA, bufB, sLD0, sLD1);
+    if (b + 1 < st.nqb) dkv_step<T, D, CAUSAL>(st, b + 1, bufB, bufA, sLD1, sLD0);
   }
-  if (wave_live && key_ok) {
+  if (st.wave_live && my_k < L) {
     T* krow = dk + (int64_t)(start + my_k) * sdk.row + (int64_t)h * sdk.head;
     T* vrow = dv + (int64_t)(start + my_k) * sdv.row + (int64_t)h * sdv.head;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
-      store_row_slice<T>(krow, 32 * dt, g, dkacc[dt], scale);
-      store_row_slice<T>(vrow, 32 * dt, g, dvacc[dt], 1.0f);
+      store_row_slice<T>(krow, 32 * dt, st.g, st.dkacc[dt], scale);
+      store_row_slice<T>(vrow, 32 * dt, st.g, st.dvacc[dt], 1.0f);
     }
   }
 }
