@@ -12,7 +12,8 @@ pass into preallocated buffers.  ``value`` is real-token causal TFLOP/s
 
 Also reported (``secondary``): config 3 forward, config 4 on the reference's
 fixed H100 length list, config 5 (bf16, 32x128) forward+backward, config 2
-RMSNorm / LayerNorm forward and backward GB/s, the user-facing autograd step,
+RMSNorm / LayerNorm forward and backward GB/s, varlen softmax forward and
+backward GB/s at the config-2 shape, the user-facing autograd step,
 and per-kernel HIP-event timings.  ``roofline`` describes the dominant kernel
 of the primary step; ``cpu_baseline`` times the numpy oracle (the reference's
 einsum call pattern) on a bounded sample of the same workload.
@@ -157,6 +158,16 @@ def time_norms(cfg, steps, warmup):
     }
     y = torch.empty_like(x)
     cases["device_copy_same_bytes"] = (lambda: y.copy_(x), 2.0 * x.numel() * x.element_size())
+    # varlen softmax along the ragged axis at the same shape (x: 19758 x 4096 bf16)
+    from scree_amd.kernels.hip import softmax as Sm
+
+    off = torch.zeros(len(cfg.lengths) + 1, dtype=torch.int32)
+    off[1:] = torch.cumsum(torch.tensor(cfg.lengths, dtype=torch.int64), 0).to(torch.int32)
+    cu = off.to(dev)
+    ys = Sm.softmax_fwd(x, cu)
+    nb = x.numel() * x.element_size()
+    cases["varlen_softmax_fwd"] = (lambda: Sm.softmax_fwd(x, cu, ys), 2.0 * nb)
+    cases["varlen_softmax_bwd"] = (lambda: Sm.softmax_bwd(ys, dy, cu), 3.0 * nb)
     out = {}
     for name, (fn, nbytes) in cases.items():
         for _ in range(warmup):

@@ -156,6 +156,25 @@ int scree_layernorm_bwd(const void* dy, const void* x, const void* weight, const
                         int dparam_dtype, int64_t rows, int64_t dim, int dtype,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ softmax
+ * Replaces scree.kernels.reference.varlen_softmax
+ * (src/scree/kernels/reference/varlen_softmax.py:13-63), whose torch branch
+ * loops over sequences on the host (:44-51); the reference has no GPU kernel.
+ * x and y are contiguous (total_tokens, features) in `dtype`: for every
+ * sequence s (rows cu_seqlens[s] .. cu_seqlens[s+1]) and feature column c,
+ * y = softmax over the sequence's rows of x[., c].  Statistics in fp32.
+ */
+int scree_varlen_softmax(const void* x, void* y, const int32_t* cu_seqlens, int batch,
+                         int64_t total_tokens, int64_t features, int dtype, void* stream);
+
+/* Gradient of scree_varlen_softmax: dx = y * (dy - sum over the sequence's
+ * rows of y * dy), per column.  No kernel in the reference: its torch branch
+ * is differentiated by autograd through torch.softmax per sequence
+ * (varlen_softmax.py:44-51). */
+int scree_varlen_softmax_bwd(const void* y, const void* dy, void* dx, const int32_t* cu_seqlens,
+                             int batch, int64_t total_tokens, int64_t features, int dtype,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

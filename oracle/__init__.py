@@ -25,6 +25,12 @@ Pinning status of every function (how a plausible mistake would be caught):
   ``F.layer_norm``, unit-RMS and zero-mean/unit-variance properties.
 * ``norms.*_bwd`` -- torch autograd of ``F.rms_norm`` / ``F.layer_norm`` and
   fp64 finite differences.
+* ``softmax.varlen_softmax`` -- the reference's two known-answer tests
+  (``tests/test_varlen_kernels.py:119-139``: per-sequence rows sum to one,
+  per-sequence numpy baseline), ``torch.softmax`` per sequence, and the
+  golden vectors (torch fp64).
+* ``softmax.varlen_softmax_bwd`` -- torch autograd through ``torch.softmax``
+  per sequence and fp64 finite differences; invariant ``sum_rows dx == 0``.
 * ``schedule.build_schedule`` -- brute-force enumeration: every (sequence,
   block) appears exactly once, costs are non-increasing, ties broken by the
   stated key.
@@ -32,4 +38,4 @@ Pinning status of every function (how a plausible mistake would be caught):
 No function is "parity unpinned".
 """
 
-from . import attention, core, norms, schedule  # noqa: F401
+from . import attention, core, norms, schedule, softmax  # noqa: F401

@@ -1,0 +1,336 @@
+// Varlen softmax along the ragged dimension (gfx950).
+//
+// Reference: src/scree/kernels/reference/varlen_softmax.py:13-63 — for every
+// sequence s (rows offsets[s] .. offsets[s+1]) and every feature column c,
+// y[r, c] = exp(x[r, c] - max_r x[., c]) / sum_r exp(x[r, c] - max_r x[., c]).
+// The reference computes it with a Python loop over sequences (torch.softmax
+// / numpy per slice); it has no GPU kernel.
+//
+// Layout: x, y contiguous (total_tokens, features).  One workgroup per
+// (sequence, column chunk): its 256 threads are `ct` column lanes (each owning
+// VEC adjacent columns, one 16-byte vector when the row allows it) times
+// `256 / ct` row lanes that stride over the sequence's rows.  Pass 1 keeps an
+// online (max, sum) per column with one exp per element; the row lanes merge
+// through LDS; pass 2 re-reads the rows (the tensor is usually still in the
+// L2 / MALL) and writes the normalised values with streaming stores.
+// Statistics are fp32 for every input dtype; y has x's dtype.
+
+#include "common.h"
+
+namespace scree {
+namespace {
+
+constexpr int kSmThreads = 256;
+constexpr int kUnroll = 4;          // rows per thread per loop trip (loads issued together)
+constexpr int64_t kSmMinBlocks = 2048;  // narrow the column lanes until the grid is this big
+constexpr float kLog2eSm = 1.4426950408889634f;
+
+// VEC columns per thread: 1 (scalar) or one 16-byte vector.
+template <typename T, int VEC>
+struct Vec {
+  static_assert(VEC == 1 || VEC * sizeof(T) == 16, "scalar or 16-byte vectors");
+  static __device__ __forceinline__ void load(const T* p, float* f) {
+    if constexpr (VEC == 1) {
+      f[0] = to_f32(*p);
+    } else {
+      const uint4 v = ld16(p);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) f[e] = elem<T>(v, e);
+    }
+  }
+  static __device__ __forceinline__ void store(T* p, const float* f) {
+    if constexpr (VEC == 1) {
+      *p = from_f32<T>(f[0]);
+    } else {
+      st16_nt(p, pack16<T>(f));
+    }
+  }
+};
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
+    const T* __restrict__ x, T* __restrict__ y, const int32_t* __restrict__ cu, int64_t total,
+    int64_t features, int ct, int chunks) {
+  __shared__ float s_m[kSmThreads * VEC];
+  __shared__ float s_l[kSmThreads * VEC];
+  const int seq = blockIdx.x / chunks, chunk = blockIdx.x - seq * chunks;
+  // offsets are clamped to [0, total]: malformed input cannot index outside x
+  const int64_t start = min<int64_t>(max<int64_t>(cu[seq], 0), total);
+  const int64_t end = min<int64_t>(max<int64_t>(cu[seq + 1], start), total);
+  const int rs = kSmThreads / ct;
+  const int tc = threadIdx.x % ct, tr = threadIdx.x / ct;
+  const int64_t col = ((int64_t)chunk * ct + tc) * VEC;
+  const bool active = col < features;  // VEC > 1 only when features % VEC == 0
+
+  float m[VEC], l[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    m[e] = -__builtin_inff();
+    l[e] = 0.f;
+  }
+  if (active) {
+    for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
+      float v[kUnroll][VEC];  // kUnroll rows' loads in flight before any math
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (r + u * rs < end) {
+          Vec<T, VEC>::load(x + (r + u * rs) * features + col, v[u]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) v[u][e] = -__builtin_inff();
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          // one exp per element: scale whichever of (sum, new term) is behind
+          const float hi = fmaxf(m[e], v[u][e]);
+          const float t = hi == -__builtin_inff()
+                              ? 0.f  // -inf so far: nothing to add (avoids -inf - -inf)
+                              : __builtin_amdgcn_exp2f((fminf(m[e], v[u][e]) - hi) * kLog2eSm);
+          l[e] = v[u][e] > m[e] ? fmaf(l[e], t, 1.0f) : l[e] + t;
+          m[e] = hi;
+        }
+    }
+  }
+  // merge the row lanes of each column (fixed order: deterministic)
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    s_m[threadIdx.x * VEC + e] = m[e];
+    s_l[threadIdx.x * VEC + e] = l[e];
+  }
+  __syncthreads();
+  if (tr == 0) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float mm = m[e];
+      for (int j = 1; j < rs; ++j) mm = fmaxf(mm, s_m[(j * ct + tc) * VEC + e]);
+      float ll = 0.f;
+      for (int j = 0; j < rs; ++j) {
+        const float mj = s_m[(j * ct + tc) * VEC + e];
+        ll += mj == -__builtin_inff() ? 0.f
+                                      : s_l[(j * ct + tc) * VEC + e] *
+                                            __builtin_amdgcn_exp2f((mj - mm) * kLog2eSm);
+      }
+      m[e] = mm;
+      l[e] = ll;
+    }
+  }
+  __syncthreads();
+  if (tr == 0) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      s_m[tc * VEC + e] = m[e];
+      s_l[tc * VEC + e] = 1.0f / l[e];
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  float mm[VEC], inv[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    mm[e] = s_m[tc * VEC + e];
+    inv[e] = s_l[tc * VEC + e];
+  }
+  for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
+    float v[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (r + u * rs < end) Vec<T, VEC>::load(x + (r + u * rs) * features + col, v[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (r + u * rs >= end) break;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        v[u][e] = __builtin_amdgcn_exp2f((v[u][e] - mm[e]) * kLog2eSm) * inv[e];
+      Vec<T, VEC>::store(y + (r + u * rs) * features + col, v[u]);
+    }
+  }
+}
+
+// Backward: dx = y * (dy - s) with s = sum over the sequence's rows of y * dy,
+// per column; same decomposition as the forward.
+template <typename T, int VEC>
+__global__ __launch_bounds__(kSmThreads) void varlen_softmax_bwd_kernel(
+    const T* __restrict__ y, const T* __restrict__ dy, T* __restrict__ dx,
+    const int32_t* __restrict__ cu, int64_t total, int64_t features, int ct, int chunks) {
+  __shared__ float s_s[kSmThreads * VEC];
+  const int seq = blockIdx.x / chunks, chunk = blockIdx.x - seq * chunks;
+  const int64_t start = min<int64_t>(max<int64_t>(cu[seq], 0), total);
+  const int64_t end = min<int64_t>(max<int64_t>(cu[seq + 1], start), total);
+  const int rs = kSmThreads / ct;
+  const int tc = threadIdx.x % ct, tr = threadIdx.x / ct;
+  const int64_t col = ((int64_t)chunk * ct + tc) * VEC;
+  const bool active = col < features;
+
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  if (active) {
+    for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
+      float a[kUnroll][VEC], b[kUnroll][VEC];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (r + u * rs < end) {
+          Vec<T, VEC>::load(y + (r + u * rs) * features + col, a[u]);
+          Vec<T, VEC>::load(dy + (r + u * rs) * features + col, b[u]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) a[u][e] = b[u][e] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(a[u][e], b[u][e], acc[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) s_s[threadIdx.x * VEC + e] = acc[e];
+  __syncthreads();
+  if (tr == 0) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float t = 0.f;
+      for (int j = 0; j < rs; ++j) t += s_s[(j * ct + tc) * VEC + e];
+      acc[e] = t;
+    }
+  }
+  __syncthreads();
+  if (tr == 0) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) s_s[tc * VEC + e] = acc[e];
+  }
+  __syncthreads();
+  if (!active) return;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = s_s[tc * VEC + e];
+  for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
+    float a[kUnroll][VEC], b[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (r + u * rs < end) {
+        Vec<T, VEC>::load(y + (r + u * rs) * features + col, a[u]);
+        Vec<T, VEC>::load(dy + (r + u * rs) * features + col, b[u]);
+      }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (r + u * rs >= end) break;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) a[u][e] = a[u][e] * (b[u][e] - acc[e]);
+      Vec<T, VEC>::store(dx + (r + u * rs) * features + col, a[u]);
+    }
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Launch shape shared by forward and backward: column lanes (a power of two,
+// at most 64) and column chunks per sequence.
+struct SmShape {
+  bool vec;
+  int ct;
+  int64_t chunks;
+};
+template <typename T>
+SmShape sm_shape(int64_t features, bool aligned, int batch) {
+  constexpr int V = 16 / sizeof(T);
+  SmShape sh;
+  sh.vec = features % V == 0 && aligned;
+  const int64_t units = sh.vec ? features / V : features;  // column vectors per row
+  sh.ct = 1;
+  while (sh.ct < units && sh.ct < 64) sh.ct <<= 1;
+  // fewer column lanes -> more chunks, more workgroups (each row segment a
+  // lane group reads stays >= 8 x 16 bytes contiguous)
+  while (sh.ct > 8 && (int64_t)batch * ((units + sh.ct - 1) / sh.ct) < kSmMinBlocks) sh.ct >>= 1;
+  sh.chunks = (units + sh.ct - 1) / sh.ct;
+  return sh;
+}
+
+template <typename T>
+int launch_softmax_bwd(const void* y, const void* dy, void* dx, const int32_t* cu, int batch,
+                       int64_t total, int64_t features, hipStream_t stream) {
+  constexpr int V = 16 / sizeof(T);
+  const SmShape sh = sm_shape<T>(features, aligned16(y) && aligned16(dy) && aligned16(dx), batch);
+  if ((int64_t)batch * sh.chunks > 0x7fffffff)
+    return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax_bwd: grid too large");
+  const dim3 grid((unsigned)(batch * sh.chunks));
+  if (sh.vec)
+    hipLaunchKernelGGL((varlen_softmax_bwd_kernel<T, V>), grid, dim3(kSmThreads), 0, stream,
+                       static_cast<const T*>(y), static_cast<const T*>(dy), static_cast<T*>(dx),
+                       cu, total, features, sh.ct, (int)sh.chunks);
+  else
+    hipLaunchKernelGGL((varlen_softmax_bwd_kernel<T, 1>), grid, dim3(kSmThreads), 0, stream,
+                       static_cast<const T*>(y), static_cast<const T*>(dy), static_cast<T*>(dx),
+                       cu, total, features, sh.ct, (int)sh.chunks);
+  return check_launch("scree_varlen_softmax_bwd");
+}
+
+template <typename T>
+int launch_softmax(const void* x, void* y, const int32_t* cu, int batch, int64_t total,
+                   int64_t features, hipStream_t stream) {
+  constexpr int V = 16 / sizeof(T);
+  const SmShape sh = sm_shape<T>(features, aligned16(x) && aligned16(y), batch);
+  if ((int64_t)batch * sh.chunks > 0x7fffffff)
+    return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: grid too large");
+  const dim3 grid((unsigned)(batch * sh.chunks));
+  if (sh.vec)
+    hipLaunchKernelGGL((varlen_softmax_kernel<T, V>), grid, dim3(kSmThreads), 0, stream,
+                       static_cast<const T*>(x), static_cast<T*>(y), cu, total, features, sh.ct,
+                       (int)sh.chunks);
+  else
+    hipLaunchKernelGGL((varlen_softmax_kernel<T, 1>), grid, dim3(kSmThreads), 0, stream,
+                       static_cast<const T*>(x), static_cast<T*>(y), cu, total, features, sh.ct,
+                       (int)sh.chunks);
+  return check_launch("scree_varlen_softmax");
+}
+
+}  // namespace
+}  // namespace scree
+
+using namespace scree;
+
+extern "C" int scree_varlen_softmax(const void* x, void* y, const int32_t* cu_seqlens, int batch,
+                                    int64_t total_tokens, int64_t features, int dtype,
+                                    void* stream) {
+  if (!x || !y || !cu_seqlens)
+    return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: null pointer");
+  if (batch < 1 || total_tokens < 0 || features < 1)
+    return set_error(SCREE_ERR_INVALID,
+                     "scree_varlen_softmax: need batch >= 1, total_tokens >= 0, features >= 1");
+  if (total_tokens == 0) return SCREE_OK;
+  if (total_tokens > ((int64_t)1 << 40) / features)
+    return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: tensor too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32: return launch_softmax<float>(x, y, cu_seqlens, batch, total_tokens, features, s);
+    case SCREE_DTYPE_F16: return launch_softmax<f16>(x, y, cu_seqlens, batch, total_tokens, features, s);
+    case SCREE_DTYPE_BF16: return launch_softmax<bf16>(x, y, cu_seqlens, batch, total_tokens, features, s);
+    default: return set_error(SCREE_ERR_UNSUPPORTED, "scree_varlen_softmax: dtype %d", dtype);
+  }
+}
+
+extern "C" int scree_varlen_softmax_bwd(const void* y, const void* dy, void* dx,
+                                        const int32_t* cu_seqlens, int batch,
+                                        int64_t total_tokens, int64_t features, int dtype,
+                                        void* stream) {
+  if (!y || !dy || !dx || !cu_seqlens)
+    return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax_bwd: null pointer");
+  if (batch < 1 || total_tokens < 0 || features < 1)
+    return set_error(SCREE_ERR_INVALID,
+                     "scree_varlen_softmax_bwd: need batch >= 1, total_tokens >= 0, features >= 1");
+  if (total_tokens == 0) return SCREE_OK;
+  if (total_tokens > ((int64_t)1 << 40) / features)
+    return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax_bwd: tensor too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32:
+      return launch_softmax_bwd<float>(y, dy, dx, cu_seqlens, batch, total_tokens, features, s);
+    case SCREE_DTYPE_F16:
+      return launch_softmax_bwd<f16>(y, dy, dx, cu_seqlens, batch, total_tokens, features, s);
+    case SCREE_DTYPE_BF16:
+      return launch_softmax_bwd<bf16>(y, dy, dx, cu_seqlens, batch, total_tokens, features, s);
+    default: return set_error(SCREE_ERR_UNSUPPORTED, "scree_varlen_softmax_bwd: dtype %d", dtype);
+  }
+}

@@ -2,7 +2,8 @@
 
 Same signatures as the reference's ``scree.kernels.reference`` functions
 (``src/scree/kernels/reference/varlen_attention.py:10``,
-``varlen_rmsnorm.py:18``, ``varlen_layernorm.py:14``), taking and returning
+``varlen_rmsnorm.py:18``, ``varlen_layernorm.py:14``, ``varlen_softmax.py:13``),
+taking and returning
 :class:`scree_amd.Array`.  They run only on ROCm device tensors -- there is no
 CPU implementation here; a host array raises ``TypeError``.  Outputs reuse
 the input's offsets, as the reference does.
@@ -53,4 +54,14 @@ def varlen_layernorm(arr: Array, weight=None, bias=None, eps: float = 1e-5) -> A
                  ragged_dim=arr.ragged_dim)
 
 
-__all__ = ["varlen_attention", "varlen_layernorm", "varlen_rmsnorm"]
+def varlen_softmax(arr: Array) -> Array:
+    """Softmax along the ragged dimension, per sequence (``varlen_softmax.py:13-63``)."""
+    from .hip import varlen_softmax_hip
+
+    if arr.ragged_dim != 0:
+        raise NotImplementedError("varlen_softmax supports ragged_dim=0 only in v0.1")
+    _require_device(arr.values, "varlen_softmax")
+    return Array(values=varlen_softmax_hip(arr.values, arr.offsets), offsets=arr.offsets, ragged_dim=0)
+
+
+__all__ = ["varlen_attention", "varlen_layernorm", "varlen_rmsnorm", "varlen_softmax"]

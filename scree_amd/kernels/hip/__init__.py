@@ -22,6 +22,7 @@ from .norms import (
     varlen_rmsnorm_hip_autograd,
     varlen_rmsnorm_hip_backward,
 )
+from .softmax import varlen_softmax_hip, varlen_softmax_hip_backward
 
 __all__ = [
     "HIP_AVAILABLE",
@@ -39,4 +40,6 @@ __all__ = [
     "varlen_rmsnorm_hip",
     "varlen_rmsnorm_hip_autograd",
     "varlen_rmsnorm_hip_backward",
+    "varlen_softmax_hip",
+    "varlen_softmax_hip_backward",
 ]

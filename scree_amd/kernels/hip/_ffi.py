@@ -47,6 +47,8 @@ _SIGNATURES = {
     "scree_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),
     "scree_layernorm_fwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _F, _I, _P]),
     "scree_layernorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),
+    "scree_varlen_softmax": (_I, [_P, _P, _P, _I, _L, _L, _I, _P]),
+    "scree_varlen_softmax_bwd": (_I, [_P, _P, _P, _P, _I, _L, _L, _I, _P]),
 }
 EXPORTED = tuple(_SIGNATURES)
 

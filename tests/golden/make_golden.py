@@ -11,6 +11,7 @@ run on the rounded inputs sees the same values.
 Conventions followed (reference file:line):
   attention scale 1/sqrt(D) and causal triu mask — reference/varlen_attention.py:31-32,122-137
   LSE = natural-log logsumexp of the scaled scores — triton/varlen_attention.py:158-162
+  softmax along the ragged axis per sequence — reference/varlen_softmax.py:44-61
   RMSNorm y = x / sqrt(mean(x^2) + eps) * w — reference/varlen_rmsnorm.py:58-65
   LayerNorm population variance, eps inside the sqrt — reference/varlen_layernorm.py:64-74
   offsets = [0, cumsum(L)] int32 — _core.py:137-138
@@ -97,6 +98,20 @@ def _norm_case(rows, dim, seed, eps):
     return out
 
 
+def _softmax_case(lengths, features, seed):
+    rng = np.random.default_rng(seed)
+    n = int(sum(lengths))
+    x = (2.0 * rng.standard_normal((n,) + features)).astype(np.float16)
+    dy = rng.standard_normal((n,) + features).astype(np.float16)
+    off = _offsets(lengths)
+    tx = torch.from_numpy(x.astype(np.float64)).requires_grad_(True)
+    parts = [torch.softmax(tx[int(off[i]):int(off[i + 1])], dim=0) for i in range(len(lengths))]
+    y = torch.cat(parts, 0)
+    y.backward(torch.from_numpy(dy.astype(np.float64)))
+    return {"lengths": np.asarray(lengths, dtype=np.int32), "offsets": off, "x": x, "dy": dy,
+            "y": y.detach().numpy().astype(np.float32), "dx": tx.grad.numpy().astype(np.float32)}
+
+
 def main() -> None:
     torch.manual_seed(0)
     edge = [1, 7, 33, 64, 65]  # a single token, sub-tile, tile edge +-1
@@ -109,6 +124,8 @@ def main() -> None:
     # (log-normal mean 128, sigma 0.6, seed 0), one of its 4 heads, fp32 inputs.
     cfg1 = _attention_case([138, 118, 187], 1, 32, True, seed=0, in_dtype=np.float32)
     np.savez_compressed(os.path.join(HERE, "attention_cfg1_slice_causal.npz"), **cfg1)
+    np.savez_compressed(os.path.join(HERE, "softmax_4x16.npz"),
+                        **_softmax_case([1, 3, 0, 17, 64, 130], (4, 16), seed=7))
     np.savez_compressed(os.path.join(HERE, "norms_37x96.npz"), **_norm_case(37, 96, seed=5, eps=1e-6))
     np.savez_compressed(os.path.join(HERE, "norms_3x4096.npz"), **_norm_case(3, 4096, seed=6, eps=1e-6))
 
