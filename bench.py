@@ -13,7 +13,8 @@ pass into preallocated buffers.  ``value`` is real-token causal TFLOP/s
 Also reported (``secondary``): config 3 forward, config 4 on the reference's
 fixed H100 length list, config 5 (bf16, 32x128) forward+backward, config 2
 RMSNorm / LayerNorm forward and backward GB/s, varlen softmax forward and
-backward GB/s at the config-2 shape, the user-facing autograd step,
+backward and packed <-> padded conversions GB/s at the config-2 shape, the
+user-facing autograd step,
 and per-kernel HIP-event timings.  ``roofline`` describes the dominant kernel
 of the primary step; ``cpu_baseline`` times the numpy oracle (the reference's
 einsum call pattern) on a bounded sample of the same workload.
@@ -168,6 +169,17 @@ def time_norms(cfg, steps, warmup):
     nb = x.numel() * x.element_size()
     cases["varlen_softmax_fwd"] = (lambda: Sm.softmax_fwd(x, cu, ys), 2.0 * nb)
     cases["varlen_softmax_bwd"] = (lambda: Sm.softmax_bwd(ys, dy, cu), 3.0 * nb)
+    # packed <-> padded at the same shape: (64, 829, 4096) bf16 padded batch
+    from scree_amd.kernels.hip import padding as Pd
+
+    max_len = max(cfg.lengths)
+    padded, pmask = Pd.to_padded_hip(x, cu, max_len=max_len)
+    row = dim * x.element_size()
+    pad_rows = len(cfg.lengths) * max_len
+    cases["to_padded"] = (lambda: Pd.to_padded_hip(x, cu, max_len=max_len),
+                          rows * row + pad_rows * (row + 1))
+    cases["from_padded_user_call"] = (lambda: Pd.from_padded_hip(padded, pmask),
+                                      pad_rows + 2.0 * rows * row)
     out = {}
     for name, (fn, nbytes) in cases.items():
         for _ in range(warmup):

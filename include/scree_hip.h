@@ -175,6 +175,35 @@ int scree_varlen_softmax_bwd(const void* y, const void* dy, void* dx, const int3
                              int batch, int64_t total_tokens, int64_t features, int dtype,
                              void* stream);
 
+/* ------------------------------------------------------------ padded <-> packed
+ * Replace the host loops of scree.to_padded / scree.from_padded
+ * (src/scree/_core.py:161-266 and :269-301; torch branch :240-266 and
+ * :278-285) and so the HF bridge built on them (src/scree/bridges/_hf_padded.py:15-46).
+ * A row is `row_bytes` bytes (one token's features, any dtype).
+ */
+
+/* padded (batch, max_len, row) and mask (batch, max_len) bytes 0/1 (may be
+ * NULL) from packed values (total_tokens, row) and int32 offsets (batch+1):
+ * row t of batch row b is value row offsets[b] + t - lo_b when lo_b <= t <
+ * lo_b + len_b (lo_b = 0, or max_len - len_b when `left`), else the fill
+ * element (`elem_bytes` bytes at host pointer `fill_elem`, repeated).
+ * Sequences longer than max_len keep their first max_len rows. */
+int scree_to_padded(const void* values, const int32_t* offsets, int batch, int64_t total_tokens,
+                    int64_t max_len, int64_t row_bytes, int left, const void* fill_elem,
+                    int elem_bytes, void* padded, void* mask, void* stream);
+
+/* offsets (batch+1, int32, device) from a (batch, max_len) byte mask: the
+ * per-row count of nonzero bytes, exclusive-scanned (the reference's
+ * lengths = mask[i].sum(), _core.py:282).  batch * max_len must fit int32. */
+int scree_padded_offsets(const void* mask, int batch, int64_t max_len, int32_t* offsets,
+                         void* stream);
+
+/* values (total_tokens, row) from padded (batch, max_len, row): value row
+ * offsets[b] + t = padded[b, t] for t < len_b (the first len_b rows of each
+ * batch row, _core.py:283-284).  total_tokens = offsets[batch]. */
+int scree_from_padded(const void* padded, const int32_t* offsets, int batch, int64_t max_len,
+                      int64_t row_bytes, int64_t total_tokens, void* values, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,11 @@ Pinning status of every function (how a plausible mistake would be caught):
   golden vectors (torch fp64).
 * ``softmax.varlen_softmax_bwd`` -- torch autograd through ``torch.softmax``
   per sequence and fp64 finite differences; invariant ``sum_rows dx == 0``.
+* ``padding.to_padded`` / ``padding.from_padded`` -- the reference's own
+  tests restated (shapes, mask sum 17, left-padding mask rows, round trip
+  identity, HF 1/0 mask rows; ``tests/test_core.py:58-78``,
+  ``tests/test_bridges.py:17-37``), and the index identity
+  ``padded[b, lo_b + t] == values[off_b + t]`` checked elementwise.
 * ``schedule.build_schedule`` -- brute-force enumeration: every (sequence,
   block) appears exactly once, costs are non-increasing, ties broken by the
   stated key.
@@ -38,4 +43,4 @@ Pinning status of every function (how a plausible mistake would be caught):
 No function is "parity unpinned".
 """
 
-from . import attention, core, norms, schedule, softmax  # noqa: F401
+from . import attention, core, norms, padding, schedule, softmax  # noqa: F401

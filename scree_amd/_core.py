@@ -133,11 +133,20 @@ def unpack(arr: Array) -> List[Any]:
 
 
 def to_padded(arr: Array, side: str = "right", fill_value: float = 0.0) -> Tuple[Any, Any]:
-    """``(padded, mask)`` with ``padded.shape == (B, max_len, *features)``."""
+    """``(padded, mask)`` with ``padded.shape == (B, max_len, *features)``.
+
+    Semantics of the reference (``_core.py:161-266``).  ROCm tensors go through
+    the device kernel; host arrays use the loop below.
+    """
     if arr.ragged_dim != 0:
         raise NotImplementedError("to_padded supports ragged_dim=0 only in v0.1")
     if side not in ("right", "left"):
         raise ValueError(f"side must be 'right' or 'left', got {side!r}")
+    if _is_torch(arr.values) and arr.values.is_cuda:
+        # ROCm tensors: one device launch (scree_to_padded), no per-row host loop
+        from .kernels.hip.padding import to_padded_hip
+
+        return to_padded_hip(arr.values, arr.offsets, side, fill_value)
     bounds = [int(o) for o in arr.offsets.tolist()]
     lengths = [bounds[i + 1] - bounds[i] for i in range(arr.batch_size)]
     max_len = max(lengths) if lengths else 0
@@ -166,8 +175,17 @@ def to_padded(arr: Array, side: str = "right", fill_value: float = 0.0) -> Tuple
 
 
 def from_padded(padded: Any, mask: Any) -> Array:
-    """Inverse of right-padded :func:`to_padded`."""
+    """Inverse of right-padded :func:`to_padded` (reference ``_core.py:269-301``).
+
+    ROCm tensors go through the device kernels; host arrays use the loop below.
+    """
     batch = padded.shape[0]
+    if _is_torch(padded) and padded.is_cuda:
+        # ROCm tensors: device count/scan + gather (scree_padded_offsets, scree_from_padded)
+        from .kernels.hip.padding import from_padded_hip
+
+        values, offsets = from_padded_hip(padded, mask)
+        return Array(values=values, offsets=offsets, ragged_dim=0)
     if _is_torch(padded):
         import torch
 

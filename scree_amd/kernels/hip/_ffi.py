@@ -49,6 +49,9 @@ _SIGNATURES = {
     "scree_layernorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),
     "scree_varlen_softmax": (_I, [_P, _P, _P, _I, _L, _L, _I, _P]),
     "scree_varlen_softmax_bwd": (_I, [_P, _P, _P, _P, _I, _L, _L, _I, _P]),
+    "scree_to_padded": (_I, [_P, _P, _I, _L, _L, _L, _I, _P, _I, _P, _P, _P]),
+    "scree_padded_offsets": (_I, [_P, _I, _L, _P, _P]),
+    "scree_from_padded": (_I, [_P, _P, _I, _L, _L, _L, _P, _P]),
 }
 EXPORTED = tuple(_SIGNATURES)
 
