@@ -214,21 +214,21 @@ template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 lds_frag16(const T* p) {
   return __builtin_bit_cast(typename VecT<T>::x8, *reinterpret_cast<const uint4*>(p));
 }
-// Transposed operand from a row-major LDS tile X[row][col] (leading dim ld).
+// Transposed operand from a row-major LDS tile X[row][col].
 // ds_read_tr16_b64 hands lane 16G + i, slot j, element i%4 of the 8 bytes
 // addressed by lane 16G + 4j + i/4.  With each lane addressing
-// X[4g + (lr%16)/4][16*(lr/16) + 4*(lr%4)] (swz_tr_off adds the tile
-// swizzle), lane (lr, g) receives X[4g + j][lr] in slots j = 0..3; a second
-// read 8 rows further gives slots 4..7.  That is the k-run layout
-// {4g + 0..3, 8 + 4g + 0..3} of the MFMA operands here (rows of X are the k
-// axis, columns the M axis).
+// X[4g + (lr%16)/4][16*(lr/16) + 4*(lr%4)] (offset `o.x` from swz_tr_off,
+// which adds the tile swizzle), lane (lr, g) receives X[4g + j][lr] in slots
+// j = 0..3; a second read 8 rows further (offset `o.y`) gives slots 4..7.
+// That is the k-run layout {4g + 0..3, 8 + 4g + 0..3} of the MFMA operands
+// here (rows of X are the k axis, columns the M axis).
 template <typename T>
-__device__ __forceinline__ typename VecT<T>::x8 lds_frag_tr(const T* p, int ld) {
+__device__ __forceinline__ typename VecT<T>::x8 lds_frag_tr(const T* base, int2 o) {
   typedef short s4 __attribute__((ext_vector_type(4)));
   typedef short s8 __attribute__((ext_vector_type(8)));
   typedef __attribute__((address_space(3))) s4* lds_s4;
-  const s4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p));
-  const s4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p + 8 * ld));
+  const s4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(base + o.x));
+  const s4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(base + o.y));
   const s8 v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   return __builtin_bit_cast(typename VecT<T>::x8, v);
 }
@@ -297,6 +297,7 @@ struct Strides {
 //    head's K/V is the L2 working set -- best when each XCD has many rounds.
 // The host picks (attn_head_major).  Returns false for blocks past the work.
 constexpr int kXcds = 8;
+
 __device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, int& item,
                                           int& head) {
   const int b = blockIdx.x;
@@ -318,20 +319,36 @@ __device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, i
 // as values <= 1 (same relative precision), and most blocks skip the O rescale.
 constexpr float kRescaleLog2Gap = 8.0f;
 
-// ---------------------------------------------------------------- forward
+// ------------------------------------------------------- tile staging
 // Direct-to-LDS tiles.  A ROWS x D tile of one head is copied from HBM into
 // an unpadded row-major LDS tile by buffer loads with an LDS destination
 // (no registers in between): each wave instruction fills one contiguous
 // 1 KB window, lane l writing bytes [16 l, 16 l + 16), so the tile's layout is
 // chosen by which global chunk each lane fetches.  The 16-byte chunk c of row
-// r is stored at chunk position c ^ swz(r); with swz below, both the 16-byte
-// row reads (8 consecutive rows, one chunk) and the transposed 8-byte reads
-// (4 consecutive rows, two adjacent chunks) touch 32 distinct banks.  The
-// buffer descriptor covers only the sequence's valid rows: rows past it are
-// written as zeros by the hardware.
+// r is stored at chunk position c ^ swz(r).
+//
+// gfx950's LDS serves 256 bytes (64 banks x 4 B) per pass; a 16-byte row read
+// (ds_read_b128) is served 16 lanes per pass, here 16 consecutive rows at one
+// logical chunk, and a transposed read (ds_read_b64_tr_b16) 32 lanes per
+// pass, here 4 consecutive rows x 64 contiguous bytes.  swz makes both
+// conflict-free (measured on MI355X: ~215 B/clk/CU for either read, against
+// ~134 with a pattern that repeats every 8 rows):
+//  * D = 64 (128-byte rows, two rows per 256 bytes): over 16 consecutive
+//    rows, swz is a bijection onto 0..7 on the even and on the odd rows;
+//    rows 4k and 4k+2 (and 4k+1, 4k+3) differ in bit 2, so their 64-byte
+//    chunk groups are disjoint.
+//  * D = 128 (256-byte rows): swz is a bijection onto 0..15 over 16 rows,
+//    and swz >> 2 differs over 4 consecutive rows.
+//  * D = 32 (64-byte rows, four per 256 bytes): rows r, r+4, r+8, r+12 take
+//    distinct values; a transposed read covers whole rows.
+// swz repeats every 16 rows, so tile offsets that are multiples of 16 rows
+// keep the same lane offsets.  The buffer descriptor covers only the
+// sequence's valid rows: rows past it are written as zeros by the hardware.
 template <int D>
 __device__ __forceinline__ int swz(int row) {
-  return D >= 64 ? 2 * (row & 3) + ((row >> 2) & 1) : 2 * ((row >> 1) & 1) + ((row >> 2) & 1);
+  return D >= 128 ? 4 * (row & 3) + ((row >> 2) & 3)
+       : D >= 64  ? 4 * ((row >> 1) & 1) + ((row >> 2) & 3)
+                  : (row >> 2) & 3;
 }
 
 template <typename T, int D, int ROWS>
@@ -376,14 +393,19 @@ template <int D>
 __device__ __forceinline__ int swz_off(int row, int c) {
   return row * D + ((c ^ swz<D>(row)) << 3);
 }
-// This lane's transposed-read offset for column block dt (32 columns): the
-// lane addresses row 4g + (lr%16)/4, column 32dt + 16(lr/16) + 4(lr%4)
-// (see lds_frag_tr); the second read, 8 rows down, has the same swizzle.
+// This lane's transposed-read offsets for column block dt (32 columns): the
+// lane addresses row 4g + (lr%16)/4 (.x) and 8 rows further (.y), column
+// 32dt + 16(lr/16) + 4(lr%4) (see lds_frag_tr).
 template <int D>
-__device__ __forceinline__ int swz_tr_off(int lr, int g, int dt) {
-  const int r = 4 * g + ((lr & 15) >> 2);
+__device__ __forceinline__ int2 swz_tr_off(int lr, int g, int dt) {
   const int c = 4 * dt + 2 * (lr >> 4) + ((lr & 3) >> 1);
-  return r * D + ((c ^ swz<D>(r)) << 3) + 4 * (lr & 1);
+  int o[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int r = 4 * g + ((lr & 15) >> 2) + 8 * half;
+    o[half] = r * D + ((c ^ swz<D>(r)) << 3) + 4 * (lr & 1);
+  }
+  return make_int2(o[0], o[1]);
 }
 
 // Reductions across the two 32-lane halves of a wave: v_permlane32_swap
@@ -420,7 +442,7 @@ struct FwdState {
   typedef typename VecT<T>::x8 x8;
   x8 qf[D / 16];            // this lane's query row, MFMA B fragments
   int koff[D / 16];         // swizzled K row-read offsets
-  int voffs[D / 32];        // swizzled V transposed-read offsets
+  int2 voffs[D / 32];       // swizzled V transposed-read offsets
   f32x16 oacc[D / 32];      // O^T accumulators
   float m_run, l_run;       // running max (raw scores) and row sum (this lane's keys)
   DmaTile<T, D, kBN> dK, dV;
@@ -497,7 +519,7 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
       const x8 pf = pack_frag<T>(sacc, 8 * hh);
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
-        st.oacc[dt] = mfma32(lds_frag_tr(sV + (32 * t + 16 * hh) * D + st.voffs[dt], D), pf,
+        st.oacc[dt] = mfma32(lds_frag_tr(sV + (32 * t + 16 * hh) * D, st.voffs[dt]), pf,
                              st.oacc[dt]);
     }
   }
@@ -596,7 +618,7 @@ struct DqState {
   typedef typename VecT<T>::x8 x8;
   x8 qf[D / 16], df[D / 16];  // this lane's Q and dO rows, MFMA B fragments
   int koff[D / 16];           // swizzled row-read offsets (K and V tiles)
-  int ktr[D / 32];            // swizzled transposed-read offsets (K^T)
+  int2 ktr[D / 32];           // swizzled transposed-read offsets (K^T)
   f32x16 dqacc[D / 32];       // dQ^T accumulators
   f32x16 neg_delta;           // dP^T accumulates onto -Delta: it comes out as dP^T - Delta
   float lse2;                 // this lane's LSE * log2(e)
@@ -642,7 +664,7 @@ __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __r
       const x8 sf = pack_frag<T>(sacc, 8 * hh);
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
-        st.dqacc[dt] = mfma32(lds_frag_tr(sK + (32 * t + 16 * hh) * D + st.ktr[dt], D), sf,
+        st.dqacc[dt] = mfma32(lds_frag_tr(sK + (32 * t + 16 * hh) * D, st.ktr[dt]), sf,
                               st.dqacc[dt]);
     }
   }
@@ -758,7 +780,7 @@ struct DkvState {
   x8 kf[D / 16], vf[D / 16];      // this lane's K and V rows, MFMA B fragments
   f32x16 dkacc[D / 32], dvacc[D / 32];
   int qoff[D / 16];               // swizzled row-read offsets (Q and dO tiles)
-  int qtr[D / 32];                // swizzled transposed-read offsets
+  int2 qtr[D / 32];               // swizzled transposed-read offsets
   DmaTile<T, D, BQ> dQ, dO;
   const T* qh;
   const T* dh;
@@ -851,9 +873,9 @@ __device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __
         const x8 sf = pack_frag<T>(sacc, 8 * hh);
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-          st.dvacc[dt] = mfma32(lds_frag_tr(sO + (32 * u + 16 * hh) * D + st.qtr[dt], D), pf,
+          st.dvacc[dt] = mfma32(lds_frag_tr(sO + (32 * u + 16 * hh) * D, st.qtr[dt]), pf,
                                 st.dvacc[dt]);
-          st.dkacc[dt] = mfma32(lds_frag_tr(sQ + (32 * u + 16 * hh) * D + st.qtr[dt], D), sf,
+          st.dkacc[dt] = mfma32(lds_frag_tr(sQ + (32 * u + 16 * hh) * D, st.qtr[dt]), sf,
                                 st.dkacc[dt]);
         }
       }
