@@ -121,6 +121,38 @@ int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k, const voi
                        int head_dim, const int64_t* strides, float softmax_scale, int causal,
                        int dtype, const void* workspace, size_t workspace_bytes, void* stream);
 
+/* Grouped-query forms of the four calls above: q, o, dout, dq, lse and delta
+ * have `heads` heads, k, v, dk and dv have `kv_heads` (a divisor of heads);
+ * query head h attends with K/V head h / (heads / kv_heads), and dk / dv sum
+ * the contributions of each group's query heads (no atomics: one workgroup
+ * owns each K/V block and sweeps its group).  With kv_heads == heads they are
+ * the calls above.  No counterpart in the reference, whose Q, K and V must
+ * share a head count (docs/kernels.md:177 lists GQA as missing); its head
+ * indexing is src/scree/kernels/triton/varlen_attention.py:64-66,84-90. */
+int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, float* lse,
+                       const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                       int kv_heads, int head_dim, const int64_t* strides, float softmax_scale,
+                       int causal, int dtype, const void* workspace, size_t workspace_bytes,
+                       void* stream);
+int scree_attn_bwd_gqa(const void* dout, const void* q, const void* k, const void* v,
+                       const void* o, const float* lse, void* dq, void* dk, void* dv, float* delta,
+                       const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                       int kv_heads, int head_dim, const int64_t* strides, float softmax_scale,
+                       int causal, int dtype, const void* workspace, size_t workspace_bytes,
+                       void* stream);
+int scree_attn_bwd_dq_gqa(const void* dout, const void* q, const void* k, const void* v,
+                          const void* o, const float* lse, void* dq, float* delta,
+                          const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                          int kv_heads, int head_dim, const int64_t* strides, float softmax_scale,
+                          int causal, int dtype, const void* workspace, size_t workspace_bytes,
+                          void* stream);
+int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const void* k, const void* v,
+                           const float* lse, const float* delta, void* dk, void* dv,
+                           const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
+                           int kv_heads, int head_dim, const int64_t* strides,
+                           float softmax_scale, int causal, int dtype, const void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* -------------------------------------------------------------------- norms
  * Replace varlen_rmsnorm_triton (src/scree/kernels/triton/varlen_rmsnorm.py:17-99)
  * and varlen_layernorm_triton (src/scree/kernels/triton/varlen_layernorm.py:14-109).

@@ -21,6 +21,11 @@ Pinning status of every function (how a plausible mistake would be caught):
   ``sum_k exp(S - LSE) == 1`` and ``torch.logsumexp``.
 * ``attention.attention_bwd`` -- torch autograd through SDPA on the same
   inputs and fp64 central finite differences; invariant ``sum_k dS == 0``.
+* grouped-query attention in the three functions above (``k`` / ``v`` with
+  fewer heads) -- torch SDPA with ``enable_gqa=True`` and its autograd per
+  sequence (a library routine that implements the grouping independently),
+  and the special case of one K/V head, where every query head must see the
+  same keys.
 * ``norms.*_fwd`` -- the reference's known-answer tests, ``F.rms_norm`` /
   ``F.layer_norm``, unit-RMS and zero-mean/unit-variance properties.
 * ``norms.*_bwd`` -- torch autograd of ``F.rms_norm`` / ``F.layer_norm`` and

@@ -20,6 +20,13 @@ GPU backward evaluates (``src/scree/kernels/triton/_backward.py:53-69`` for
     dP = dO V^T                 dS = P * (dP - Delta)
     dQ = scale * dS K           dK = scale * dS^T Q
 
+Grouped-query attention (``k`` / ``v`` with ``kv_heads`` dividing the
+query heads; no counterpart in the reference, whose docs list it as missing,
+``docs/kernels.md:177``) is defined by its identity with ordinary attention:
+each K/V head is repeated for the ``g = heads // kv_heads`` consecutive query
+heads of its group (query head ``h`` uses K/V head ``h // g``), and ``dK`` /
+``dV`` are the repeated-head gradients summed over each group.
+
 ``impl="einsum"`` reproduces the reference's call pattern (``np.einsum``
 without ``optimize``: single-threaded loops, the CPU baseline);
 ``impl="matmul"`` evaluates the same sums through ``np.matmul`` and is what
@@ -55,14 +62,32 @@ def _pv(attn, vi, impl):
     return np.matmul(attn, vi.transpose(1, 0, 2)).transpose(1, 0, 2)
 
 
+def _expand_kv(t, heads):
+    """Repeat each K/V head for the consecutive query heads of its group."""
+    hkv = t.shape[1]
+    if hkv == heads:
+        return t
+    if hkv < 1 or heads % hkv:
+        raise ValueError("k/v heads must divide q heads")
+    return np.repeat(t, heads // hkv, axis=1)
+
+
+def _fold_kv(t, kv_heads):
+    """Sum repeated-head gradients back onto their K/V head."""
+    n, h, d = t.shape
+    if h == kv_heads:
+        return t
+    return t.reshape(n, kv_heads, h // kv_heads, d).sum(axis=2)
+
+
 def attention_fwd(q, k, v, offsets, causal=False, dtype=np.float64, impl="matmul",
                   k_offsets=None, v_offsets=None):
     """Return ``(O, LSE)`` for packed ``q, k, v`` of shape ``(N, H, D)``."""
     off = _check_offsets(offsets, offsets if k_offsets is None else k_offsets,
                          offsets if v_offsets is None else v_offsets)
     q = np.asarray(q, dtype=dtype)
-    k = np.asarray(k, dtype=dtype)
-    v = np.asarray(v, dtype=dtype)
+    k = _expand_kv(np.asarray(k, dtype=dtype), q.shape[1])
+    v = _expand_kv(np.asarray(v, dtype=dtype), q.shape[1])
     n, h, d = q.shape
     scale = 1.0 / math.sqrt(d)
     out = np.zeros_like(q)
@@ -87,7 +112,7 @@ def attention_fwd(q, k, v, offsets, causal=False, dtype=np.float64, impl="matmul
 def attention_lse(q, k, offsets, causal=False, dtype=np.float64):
     """LSE alone, computed independently of the forward's running max."""
     q = np.asarray(q, dtype=dtype)
-    k = np.asarray(k, dtype=dtype)
+    k = _expand_kv(np.asarray(k, dtype=dtype), q.shape[1])
     off = np.asarray(offsets, dtype=np.int64)
     n, h, d = q.shape
     scale = 1.0 / math.sqrt(d)
@@ -107,8 +132,9 @@ def attention_bwd(do, q, k, v, o, lse, offsets, causal=False, dtype=np.float64, 
     off = np.asarray(offsets, dtype=np.int64)
     do = np.asarray(do, dtype=dtype)
     q = np.asarray(q, dtype=dtype)
-    k = np.asarray(k, dtype=dtype)
-    v = np.asarray(v, dtype=dtype)
+    kv_heads = np.shape(k)[1]
+    k = _expand_kv(np.asarray(k, dtype=dtype), q.shape[1])
+    v = _expand_kv(np.asarray(v, dtype=dtype), q.shape[1])
     o = np.asarray(o, dtype=dtype)
     lse = np.asarray(lse, dtype=dtype)
     n, h, d = q.shape
@@ -141,4 +167,4 @@ def attention_bwd(do, q, k, v, o, lse, offsets, causal=False, dtype=np.float64, 
         else:
             dq[s:e] = scale * np.matmul(ds, ki.transpose(1, 0, 2)).transpose(1, 0, 2)
             dk[s:e] = scale * np.matmul(ds.transpose(0, 2, 1), qi.transpose(1, 0, 2)).transpose(1, 0, 2)
-    return dq, dk, dv, delta
+    return dq, _fold_kv(dk, kv_heads), _fold_kv(dv, kv_heads), delta

@@ -296,20 +296,28 @@ struct Strides {
 //    ... one at a time, each in the scheduler's longest-first order, so one
 //    head's K/V is the L2 working set -- best when each XCD has many rounds.
 // The host picks (attn_head_major).  Returns false for blocks past the work.
+//
+// Grouped-query attention (group > 1 query heads per K/V head): with heads a
+// multiple of 8 the head index is permuted so that XCD x serves the
+// contiguous heads x*heads/8 .. (x+1)*heads/8 - 1 instead of x, x+8, ...;
+// when group divides heads/8, every group then shares one XCD and its K/V
+// stays in that XCD's L2.
 constexpr int kXcds = 8;
 
-__device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, int& item,
-                                          int& head) {
+__device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, int group,
+                                          int& item, int& head) {
   const int b = blockIdx.x;
   if (head_major) {
     const int x = b % kXcds, j = b / kXcds;
     const int k = j / tmax;  // k-th head of this XCD
     item = j - k * tmax;
     head = x + kXcds * k;
-    return head < heads;
+    if (head >= heads) return false;
+  } else {
+    item = b / heads;
+    head = b % heads;
   }
-  item = b / heads;
-  head = b % heads;
+  if (group > 1 && heads % kXcds == 0) head = (head % kXcds) * (heads / kXcds) + head / kXcds;
   return true;
 }
 
@@ -531,14 +539,15 @@ template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, const int32_t* __restrict__ header, const int4* __restrict__ items,
-    int tmax, int head_major, int heads, Strides sq, Strides sk, Strides sv, Strides so,
-    float scale, float scale_log2) {
+    int tmax, int head_major, int heads, int group, Strides sq, Strides sk, Strides sv,
+    Strides so, float scale, float scale_log2) {
   constexpr int TILE = kBN * D;  // elements per K or V tile
   constexpr int BUF = 2 * TILE;  // one buffer: K tile then V tile
   __shared__ __align__(16) T smem[2 * BUF];
 
   int item, h;
-  if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
+  if (!map_block(heads, tmax, head_major, group, item, h) || item >= header[0]) return;
+  const int hk = h / group;  // K/V head of this query head
   const int4 it = items[item];
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   FwdState<T, D> st;
@@ -550,8 +559,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   const int my_q = st.qw0 + st.lr;
   const bool wave_live = st.qw0 < L;
   st.L = L;
-  st.kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
-  st.vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
+  st.kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
+  st.vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
   st.krow = sk.row;
   st.vrow = sv.row;
   const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
@@ -677,15 +686,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
     float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq,
-    Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2) {
+    const int4* __restrict__ items, int tmax, int head_major, int heads, int group, Strides sdo,
+    Strides sq, Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2) {
   typedef typename VecT<T>::x8 x8;
   constexpr int TILE = kBN * D;
   constexpr int BUF = 2 * TILE;  // K tile then V tile
   __shared__ __align__(16) T smem[2 * BUF];
 
   int item, h;
-  if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
+  if (!map_block(heads, tmax, head_major, group, item, h) || item >= header[0]) return;
+  const int hk = h / group;  // K/V head of this query head
   const int4 it = items[item];
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   DqState<T, D> st;
@@ -697,8 +707,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   const int my_q = st.qw0 + st.lr;
   const bool wave_live = st.qw0 < L;
   st.L = L;
-  st.kh = k + (int64_t)start * sk.row + (int64_t)h * sk.head;
-  st.vh = v + (int64_t)start * sv.row + (int64_t)h * sv.head;
+  st.kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
+  st.vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
   st.krow = sk.row;
   st.vrow = sv.row;
   const int kend_wg = CAUSAL ? min(L, q0 + kBM) : L;
@@ -902,8 +912,9 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
     T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int tmax, int head_major, int heads, Strides sdo, Strides sq,
-    Strides sk, Strides sv, Strides sdk, Strides sdv, float scale, float scale_log2) {
+    const int4* __restrict__ items, int tmax, int head_major, int kv_heads, int group,
+    Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk, Strides sdv, float scale,
+    float scale_log2) {
   constexpr int BQ = dkv_bq<D>();
   constexpr int TILE = BQ * D;
   constexpr int BUF = 2 * TILE;  // Q tile then dO tile
@@ -915,8 +926,12 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
   float* sLD0 = reinterpret_cast<float*>(smem + 2 * BUF);
   float* sLD1 = reinterpret_cast<float*>(smem + 2 * BUF + ROWS_T);
 
-  int item, h;
-  if (!map_block(heads, tmax, head_major, item, h) || item >= header[0]) return;
+  // One workgroup per (item, K/V head hk); the group's query heads
+  // hk*group .. hk*group + group - 1 are swept one after another and their
+  // contributions accumulate in the dK / dV registers.
+  int item, hk;
+  if (!map_block(kv_heads, tmax, head_major, 1, item, hk) || item >= header[0]) return;
+  const int heads = kv_heads * group;
   const int4 it = items[item];
   const int start = it.z, L = it.w;
   const int nblk = (L + kBM - 1) / kBM;
@@ -931,12 +946,8 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
   st.wave_live = st.kw0 < L;
   st.L = L;
   st.heads = heads;
-  st.qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
-  st.dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
   st.qrow = sq.row;
   st.drow = sdo.row;
-  st.lse_h = lse + (int64_t)start * heads + h;
-  st.delta_h = delta + (int64_t)start * heads + h;
   st.qbeg = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
   st.nqb = (L - st.qbeg + BQ - 1) / BQ;
   st.scale_log2 = scale_log2;
@@ -945,16 +956,24 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
   T* bufB = smem + BUF;
   st.dQ.init(sq.row, st.wave, lane);
   st.dO.init(sdo.row, st.wave, lane);
-  st.dQ.load(bufA, st.qh, sq.row, st.qbeg, L, st.wave);
-  st.dO.load(bufA + TILE, st.dh, sdo.row, st.qbeg, L, st.wave);
-  if (threadIdx.x < BQ) {
-    dkv_load_rows(st, st.qbeg + (int)threadIdx.x);
-    dkv_store_rows(sLD0, BQ, st.pl, st.pd);
-  }
+  // Query head h: point the state at it and stage its first block.
+  auto start_head = [&](int h) {
+    st.qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
+    st.dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
+    st.lse_h = lse + (int64_t)start * heads + h;
+    st.delta_h = delta + (int64_t)start * heads + h;
+    st.dQ.load(bufA, st.qh, sq.row, st.qbeg, L, st.wave);
+    st.dO.load(bufA + TILE, st.dh, sdo.row, st.qbeg, L, st.wave);
+    if (threadIdx.x < BQ) {
+      dkv_load_rows(st, st.qbeg + (int)threadIdx.x);
+      dkv_store_rows(sLD0, BQ, st.pl, st.pd);
+    }
+  };
+  start_head(hk * group);
   {  // keys past L read row L-1: their results are never stored
     const int64_t tok = start + min(my_k, L - 1);
-    const T* krow = k + tok * sk.row + (int64_t)h * sk.head;
-    const T* vrow = v + tok * sv.row + (int64_t)h * sv.head;
+    const T* krow = k + tok * sk.row + (int64_t)hk * sk.head;
+    const T* vrow = v + tok * sv.row + (int64_t)hk * sv.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
       st.kf[s] = gmem_frag16(krow + 16 * s + 8 * st.g);
@@ -976,16 +995,21 @@ __global__ __launch_bounds__(kThreads, D >= 128 ? 1 : 2) void attn_bwd_dkv_kerne
     st.dvacc[dt] = zero16();
   }
 
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  // Unrolled by two so that each call sees its buffers at fixed positions.
-  for (int b = 0; b < st.nqb; b += 2) {
-    dkv_step<T, D, CAUSAL>(st, b, bufA, bufB, sLD0, sLD1);
-    if (b + 1 < st.nqb) dkv_step<T, D, CAUSAL>(st, b + 1, bufB, bufA, sLD1, sLD0);
+  for (int gi = 0;;) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // Unrolled by two so that each call sees its buffers at fixed positions.
+    for (int b = 0; b < st.nqb; b += 2) {
+      dkv_step<T, D, CAUSAL>(st, b, bufA, bufB, sLD0, sLD1);
+      if (b + 1 < st.nqb) dkv_step<T, D, CAUSAL>(st, b + 1, bufB, bufA, sLD1, sLD0);
+    }
+    // The last step ended with a barrier: both buffers are free again.
+    if (++gi == group) break;
+    start_head(hk * group + gi);
   }
   if (st.wave_live && my_k < L) {
-    T* krow = dk + (int64_t)(start + my_k) * sdk.row + (int64_t)h * sdk.head;
-    T* vrow = dv + (int64_t)(start + my_k) * sdv.row + (int64_t)h * sdv.head;
+    T* krow = dk + (int64_t)(start + my_k) * sdk.row + (int64_t)hk * sdk.head;
+    T* vrow = dv + (int64_t)(start + my_k) * sdv.row + (int64_t)hk * sdv.head;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
       store_row_slice<T>(krow, 32 * dt, st.g, st.dkacc[dt], scale);
@@ -1047,23 +1071,23 @@ inline int attn_head_major(int heads, int tmax) {
 
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
-                  const int32_t* cu, int heads, const int64_t* st, float scale, int tmax,
-                  const void* ws, hipStream_t stream) {
+                  const int32_t* cu, int heads, int kv_heads, const int64_t* st, float scale,
+                  int tmax, const void* ws, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(o), lse, header, items, tmax, attn_head_major(heads, tmax), heads, Strides{st[0], st[1]},
-                     Strides{st[2], st[3]}, Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale,
-                     scale * kLog2e);
+                     static_cast<T*>(o), lse, header, items, tmax, attn_head_major(heads, tmax),
+                     heads, heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
+                     Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e);
 }
 
 // strides: {dout, q, k, v, o, dq} x {row, head}
 template <typename T, int D, bool C>
 void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
                      const float* lse, void* dq, float* delta, const int32_t* cu, int heads,
-                     const int64_t* st, float scale, int tmax, const void* ws,
+                     int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                      hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
@@ -1072,7 +1096,8 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<const T*>(o), lse, delta, static_cast<T*>(dq), header, items,
-                     tmax, attn_head_major(heads, tmax), heads, Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
+                     tmax, attn_head_major(heads, tmax), heads, heads / kv_heads,
+                     Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
                      scale * kLog2e);
 }
@@ -1081,15 +1106,16 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
 template <typename T, int D, bool C>
 void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
                       const float* lse, const float* delta, void* dk, void* dv, const int32_t* cu,
-                      int heads, const int64_t* st, float scale, int tmax, const void* ws,
-                      hipStream_t stream) {
-  const int64_t grid = (int64_t)tmax * heads;
+                      int heads, int kv_heads, const int64_t* st, float scale, int tmax,
+                      const void* ws, hipStream_t stream) {
+  const int64_t grid = (int64_t)tmax * kv_heads;  // one workgroup per (item, K/V head)
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
   hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0,
                      stream, static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), lse, delta,
-                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, tmax, attn_head_major(heads, tmax), heads,
+                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, tmax,
+                     attn_head_major(kv_heads, tmax), kv_heads, heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
                      scale * kLog2e);
@@ -1145,28 +1171,12 @@ extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t
   return check_launch(fn);
 }
 
-extern "C" int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
-                              const int32_t* cu_seqlens, int batch, int64_t total_tokens,
-                              int heads, int head_dim, const int64_t* strides, float softmax_scale,
-                              int causal, int dtype, const void* workspace,
-                              size_t workspace_bytes, void* stream) {
-  const char* fn = "scree_attn_fwd";
-  int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
-                        workspace_bytes);
-  if (rc) return rc;
-  if (!strides) return set_error(SCREE_ERR_INVALID, "%s: strides is null", fn);
-  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
-  const char* names[4] = {"q", "k", "v", "o"};
-  const void* ptrs[4] = {q, k, v, o};
-  for (int i = 0; i < 4; ++i) {
-    rc = check_tensor(fn, names[i], ptrs[i], strides + 2 * i, heads, head_dim, total_tokens);
-    if (rc) return rc;
-  }
-  if (total_tokens == 0) return SCREE_OK;
-  const int tmax = (int)tmax_for(batch, total_tokens);
-  SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, heads,
-                 strides, softmax_scale, tmax, workspace, static_cast<hipStream_t>(stream));
-  return check_launch(fn);
+static int check_heads(const char* fn, int heads, int kv_heads) {
+  if (kv_heads < 1 || kv_heads > heads || heads % kv_heads)
+    return set_error(SCREE_ERR_INVALID,
+                     "%s: kv_heads (%d) must divide heads (%d) and be at least 1", fn, kv_heads,
+                     heads);
+  return SCREE_OK;
 }
 
 static int check_bwd_tensors(const char* fn, const char* const* names, const void* const* ptrs,
@@ -1180,16 +1190,55 @@ static int check_bwd_tensors(const char* fn, const char* const* names, const voi
   return SCREE_OK;
 }
 
-extern "C" int scree_attn_bwd_dq(const void* dout, const void* q, const void* k, const void* v,
-                                 const void* o, const float* lse, void* dq, float* delta,
-                                 const int32_t* cu_seqlens, int batch, int64_t total_tokens,
-                                 int heads, int head_dim, const int64_t* strides,
-                                 float softmax_scale, int causal, int dtype,
-                                 const void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
+                                  float* lse, const int32_t* cu_seqlens, int batch,
+                                  int64_t total_tokens, int heads, int kv_heads, int head_dim,
+                                  const int64_t* strides, float softmax_scale, int causal,
+                                  int dtype, const void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  const char* fn = "scree_attn_fwd";
+  int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
+                        workspace_bytes);
+  if (rc) return rc;
+  if ((rc = check_heads(fn, heads, kv_heads))) return rc;
+  if (!strides) return set_error(SCREE_ERR_INVALID, "%s: strides is null", fn);
+  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  const char* names[4] = {"q", "k", "v", "o"};
+  const void* ptrs[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    rc = check_tensor(fn, names[i], ptrs[i], strides + 2 * i, heads, head_dim, total_tokens);
+    if (rc) return rc;
+  }
+  if (total_tokens == 0) return SCREE_OK;
+  const int tmax = (int)tmax_for(batch, total_tokens);
+  SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, heads,
+                 kv_heads, strides, softmax_scale, tmax, workspace,
+                 static_cast<hipStream_t>(stream));
+  return check_launch(fn);
+}
+
+extern "C" int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                              const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                              int heads, int head_dim, const int64_t* strides, float softmax_scale,
+                              int causal, int dtype, const void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  return scree_attn_fwd_gqa(q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, heads,
+                            head_dim, strides, softmax_scale, causal, dtype, workspace,
+                            workspace_bytes, stream);
+}
+
+extern "C" int scree_attn_bwd_dq_gqa(const void* dout, const void* q, const void* k,
+                                     const void* v, const void* o, const float* lse, void* dq,
+                                     float* delta, const int32_t* cu_seqlens, int batch,
+                                     int64_t total_tokens, int heads, int kv_heads, int head_dim,
+                                     const int64_t* strides, float softmax_scale, int causal,
+                                     int dtype, const void* workspace, size_t workspace_bytes,
+                                     void* stream) {
   const char* fn = "scree_attn_bwd_dq";
   int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
                         workspace_bytes);
   if (rc) return rc;
+  if ((rc = check_heads(fn, heads, kv_heads))) return rc;
   if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
   if (!delta || !aligned16(delta))
     return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
@@ -1200,21 +1249,34 @@ extern "C" int scree_attn_bwd_dq(const void* dout, const void* q, const void* k,
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
-                 cu_seqlens, heads, strides, softmax_scale, tmax, workspace,
+                 cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
-extern "C" int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k, const void* v,
-                                  const float* lse, const float* delta, void* dk, void* dv,
-                                  const int32_t* cu_seqlens, int batch, int64_t total_tokens,
-                                  int heads, int head_dim, const int64_t* strides,
-                                  float softmax_scale, int causal, int dtype,
-                                  const void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int scree_attn_bwd_dq(const void* dout, const void* q, const void* k, const void* v,
+                                 const void* o, const float* lse, void* dq, float* delta,
+                                 const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                                 int heads, int head_dim, const int64_t* strides,
+                                 float softmax_scale, int causal, int dtype,
+                                 const void* workspace, size_t workspace_bytes, void* stream) {
+  return scree_attn_bwd_dq_gqa(dout, q, k, v, o, lse, dq, delta, cu_seqlens, batch, total_tokens,
+                               heads, heads, head_dim, strides, softmax_scale, causal, dtype,
+                               workspace, workspace_bytes, stream);
+}
+
+extern "C" int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const void* k,
+                                      const void* v, const float* lse, const float* delta,
+                                      void* dk, void* dv, const int32_t* cu_seqlens, int batch,
+                                      int64_t total_tokens, int heads, int kv_heads,
+                                      int head_dim, const int64_t* strides, float softmax_scale,
+                                      int causal, int dtype, const void* workspace,
+                                      size_t workspace_bytes, void* stream) {
   const char* fn = "scree_attn_bwd_dkv";
   int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
                         workspace_bytes);
   if (rc) return rc;
+  if ((rc = check_heads(fn, heads, kv_heads))) return rc;
   if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
   if (!delta || !aligned16(delta))
     return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
@@ -1225,9 +1287,42 @@ extern "C" int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_bwd_dkv_t, dtype, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
-                 cu_seqlens, heads, strides, softmax_scale, tmax, workspace,
+                 cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
+}
+
+extern "C" int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k, const void* v,
+                                  const float* lse, const float* delta, void* dk, void* dv,
+                                  const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                                  int heads, int head_dim, const int64_t* strides,
+                                  float softmax_scale, int causal, int dtype,
+                                  const void* workspace, size_t workspace_bytes, void* stream) {
+  return scree_attn_bwd_dkv_gqa(dout, q, k, v, lse, delta, dk, dv, cu_seqlens, batch,
+                                total_tokens, heads, heads, head_dim, strides, softmax_scale,
+                                causal, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int scree_attn_bwd_gqa(const void* dout, const void* q, const void* k, const void* v,
+                                  const void* o, const float* lse, void* dq, void* dk, void* dv,
+                                  float* delta, const int32_t* cu_seqlens, int batch,
+                                  int64_t total_tokens, int heads, int kv_heads, int head_dim,
+                                  const int64_t* strides, float softmax_scale, int causal,
+                                  int dtype, const void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (!strides) return set_error(SCREE_ERR_INVALID, "scree_attn_bwd: strides is null");
+  // strides: {dout, q, k, v, o, dq, dk, dv} x {row, head}
+  const int64_t sdq[12] = {strides[0], strides[1], strides[2], strides[3], strides[4], strides[5],
+                           strides[6], strides[7], strides[8], strides[9], strides[10], strides[11]};
+  const int64_t sdkv[12] = {strides[0], strides[1], strides[2],  strides[3],  strides[4],  strides[5],
+                            strides[6], strides[7], strides[12], strides[13], strides[14], strides[15]};
+  int rc = scree_attn_bwd_dq_gqa(dout, q, k, v, o, lse, dq, delta, cu_seqlens, batch,
+                                 total_tokens, heads, kv_heads, head_dim, sdq, softmax_scale,
+                                 causal, dtype, workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  return scree_attn_bwd_dkv_gqa(dout, q, k, v, lse, delta, dk, dv, cu_seqlens, batch,
+                                total_tokens, heads, kv_heads, head_dim, sdkv, softmax_scale,
+                                causal, dtype, workspace, workspace_bytes, stream);
 }
 
 extern "C" int scree_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
@@ -1236,17 +1331,7 @@ extern "C" int scree_attn_bwd(const void* dout, const void* q, const void* k, co
                               int64_t total_tokens, int heads, int head_dim,
                               const int64_t* strides, float softmax_scale, int causal, int dtype,
                               const void* workspace, size_t workspace_bytes, void* stream) {
-  if (!strides) return set_error(SCREE_ERR_INVALID, "scree_attn_bwd: strides is null");
-  // strides: {dout, q, k, v, o, dq, dk, dv} x {row, head}
-  const int64_t sdq[12] = {strides[0], strides[1], strides[2], strides[3], strides[4], strides[5],
-                           strides[6], strides[7], strides[8], strides[9], strides[10], strides[11]};
-  const int64_t sdkv[12] = {strides[0], strides[1], strides[2],  strides[3],  strides[4],  strides[5],
-                            strides[6], strides[7], strides[12], strides[13], strides[14], strides[15]};
-  int rc = scree_attn_bwd_dq(dout, q, k, v, o, lse, dq, delta, cu_seqlens, batch, total_tokens,
-                             heads, head_dim, sdq, softmax_scale, causal, dtype, workspace,
-                             workspace_bytes, stream);
-  if (rc) return rc;
-  return scree_attn_bwd_dkv(dout, q, k, v, lse, delta, dk, dv, cu_seqlens, batch, total_tokens,
-                            heads, head_dim, sdkv, softmax_scale, causal, dtype, workspace,
-                            workspace_bytes, stream);
+  return scree_attn_bwd_gqa(dout, q, k, v, o, lse, dq, dk, dv, delta, cu_seqlens, batch,
+                            total_tokens, heads, heads, head_dim, strides, softmax_scale, causal,
+                            dtype, workspace, workspace_bytes, stream);
 }

@@ -21,7 +21,12 @@ def _require_device(values, fn: str) -> None:
 
 
 def varlen_attention(q: Array, k: Array, v: Array, causal: bool = False) -> Array:
-    """Per-sequence self-attention of packed ``(total, heads, head_dim)`` arrays."""
+    """Per-sequence self-attention of packed ``(total, heads, head_dim)`` arrays.
+
+    ``k`` / ``v`` may carry fewer heads than ``q`` (grouped-query attention:
+    a divisor of the query heads, each K/V head serving consecutive query
+    heads); the reference requires equal head counts.
+    """
     import torch
 
     from .hip import varlen_attention_hip_autograd

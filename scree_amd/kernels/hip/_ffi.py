@@ -42,6 +42,13 @@ _SIGNATURES = {
                                _S, _P]),
     "scree_attn_bwd_dkv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I, _P,
                                 _S, _P]),
+    "scree_attn_fwd_gqa": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F, _I, _I, _P, _S, _P]),
+    "scree_attn_bwd_gqa": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F,
+                                _I, _I, _P, _S, _P]),
+    "scree_attn_bwd_dq_gqa": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F, _I,
+                                   _I, _P, _S, _P]),
+    "scree_attn_bwd_dkv_gqa": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F, _I,
+                                    _I, _P, _S, _P]),
     "scree_norm_bwd_workspace_bytes": (_S, [_L, _L]),
     "scree_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _L, _L, _F, _I, _P]),
     "scree_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),

@@ -17,6 +17,11 @@ Differences a caller can observe:
   ``cu_seqlens`` into a work list (:func:`attention_schedule`).
 * head_dim must be 32, 64 or 128; q/k/v may be strided views whose last axis
   is contiguous (other layouts are copied to contiguous first).
+* Grouped-query attention: ``k`` / ``v`` may have fewer heads than ``q`` (a
+  divisor of its head count); query head ``h`` attends with K/V head
+  ``h // (q_heads // kv_heads)`` and ``dk`` / ``dv`` sum over each group.
+  The reference requires equal shapes (its docs list GQA as missing,
+  ``docs/kernels.md:177``); equal shapes behave exactly as there.
 """
 
 from __future__ import annotations
@@ -29,7 +34,12 @@ from . import _ffi
 
 
 def _check_inputs(q, k, v):
-    assert q.shape == k.shape == v.shape, "q, k, v must have identical shape"
+    assert k.shape == v.shape, "k and v must have identical shape"
+    assert q.dim() == 3 and k.dim() == 3, "q, k, v must be (total_tokens, n_heads, head_dim)"
+    assert q.shape[0] == k.shape[0] and q.shape[2] == k.shape[2], (
+        "q, k, v must share total_tokens and head_dim")
+    assert k.shape[1] >= 1 and q.shape[1] % k.shape[1] == 0, (
+        "k/v heads must divide q heads (grouped-query attention)")
     assert q.is_cuda, "varlen_attention_hip requires ROCm device tensors"
     assert q.dtype in (torch.float16, torch.bfloat16), "fp16 or bf16 only"
     assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
@@ -97,9 +107,9 @@ def _attn_fwd(q, k, v, cu, causal, out, lse, workspace):
     total, heads, head_dim = q.shape
     strides = _ffi.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1),
                                 v.stride(0), v.stride(1), out.stride(0), out.stride(1)])
-    _ffi.check(lib.scree_attn_fwd(
+    _ffi.check(lib.scree_attn_fwd_gqa(
         _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(out), _ffi.ptr(lse), _ffi.ptr(cu),
-        cu.numel() - 1, total, heads, head_dim, strides, 1.0 / math.sqrt(head_dim),
+        cu.numel() - 1, total, heads, k.shape[1], head_dim, strides, 1.0 / math.sqrt(head_dim),
         int(bool(causal)), _ffi.dtype_code(q.dtype), _ffi.ptr(workspace), workspace.numel(),
         _ffi.stream_of(q)))
 
@@ -109,10 +119,10 @@ def _attn_bwd(do, q, k, v, o, lse, cu, causal, dq, dk, dv, delta, workspace):
     total, heads, head_dim = q.shape
     ts = (do, q, k, v, o, dq, dk, dv)
     strides = _ffi.int64_array([s for t in ts for s in (t.stride(0), t.stride(1))])
-    _ffi.check(lib.scree_attn_bwd(
+    _ffi.check(lib.scree_attn_bwd_gqa(
         _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(o), _ffi.ptr(lse),
         _ffi.ptr(dq), _ffi.ptr(dk), _ffi.ptr(dv), _ffi.ptr(delta), _ffi.ptr(cu),
-        cu.numel() - 1, total, heads, head_dim, strides, 1.0 / math.sqrt(head_dim),
+        cu.numel() - 1, total, heads, k.shape[1], head_dim, strides, 1.0 / math.sqrt(head_dim),
         int(bool(causal)), _ffi.dtype_code(q.dtype), _ffi.ptr(workspace), workspace.numel(),
         _ffi.stream_of(q)))
 
@@ -121,22 +131,22 @@ def _attn_bwd_dq(do, q, k, v, o, lse, cu, causal, dq, delta, workspace):
     lib = _ffi.lib()
     total, heads, head_dim = q.shape
     strides = _ffi.int64_array([s for t in (do, q, k, v, o, dq) for s in (t.stride(0), t.stride(1))])
-    _ffi.check(lib.scree_attn_bwd_dq(
+    _ffi.check(lib.scree_attn_bwd_dq_gqa(
         _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(o), _ffi.ptr(lse),
-        _ffi.ptr(dq), _ffi.ptr(delta), _ffi.ptr(cu), cu.numel() - 1, total, heads, head_dim,
-        strides, 1.0 / math.sqrt(head_dim), int(bool(causal)), _ffi.dtype_code(q.dtype),
-        _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(q)))
+        _ffi.ptr(dq), _ffi.ptr(delta), _ffi.ptr(cu), cu.numel() - 1, total, heads, k.shape[1],
+        head_dim, strides, 1.0 / math.sqrt(head_dim), int(bool(causal)),
+        _ffi.dtype_code(q.dtype), _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(q)))
 
 
 def _attn_bwd_dkv(do, q, k, v, lse, delta, cu, causal, dk, dv, workspace):
     lib = _ffi.lib()
     total, heads, head_dim = q.shape
     strides = _ffi.int64_array([s for t in (do, q, k, v, dk, dv) for s in (t.stride(0), t.stride(1))])
-    _ffi.check(lib.scree_attn_bwd_dkv(
+    _ffi.check(lib.scree_attn_bwd_dkv_gqa(
         _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(lse), _ffi.ptr(delta),
-        _ffi.ptr(dk), _ffi.ptr(dv), _ffi.ptr(cu), cu.numel() - 1, total, heads, head_dim,
-        strides, 1.0 / math.sqrt(head_dim), int(bool(causal)), _ffi.dtype_code(q.dtype),
-        _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(q)))
+        _ffi.ptr(dk), _ffi.ptr(dv), _ffi.ptr(cu), cu.numel() - 1, total, heads, k.shape[1],
+        head_dim, strides, 1.0 / math.sqrt(head_dim), int(bool(causal)),
+        _ffi.dtype_code(q.dtype), _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(q)))
 
 
 def varlen_attention_hip(q, k, v, cu_seqlens, causal: bool = False, block_m: int = 64,

@@ -19,16 +19,22 @@ pytestmark = pytest.mark.gpu
 EDGE_LENGTHS = [1, 63, 64, 65, 127, 128, 129, 255, 300, 2]
 
 
-def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True):
-    say(f"case: lengths[:6]={lengths[:6]} B={len(lengths)} N={sum(lengths)} H={heads} D={dim} "
-        f"{dtype} causal={causal}")
+def _fold(t, kv_heads):
+    n, h, d = t.shape
+    return t.reshape(n, kv_heads, h // kv_heads, d).sum(axis=2)
+
+
+def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True, kv_heads=None):
+    kv_heads = heads if kv_heads is None else kv_heads
+    say(f"case: lengths[:6]={lengths[:6]} B={len(lengths)} N={sum(lengths)} H={heads} "
+        f"Hkv={kv_heads} D={dim} {dtype} causal={causal}")
     from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
 
     n = sum(lengths)
     off, cu = cu_of(lengths)
     q = randn((n, heads, dim), dtype, seed)
-    k = randn((n, heads, dim), dtype, seed + 1)
-    v = randn((n, heads, dim), dtype, seed + 2)
+    k = randn((n, kv_heads, dim), dtype, seed + 1)
+    v = randn((n, kv_heads, dim), dtype, seed + 2)
     out, lse = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True)
     torch.cuda.synchronize()
     q64, k64, v64 = np64(q), np64(k), np64(v)
@@ -37,7 +43,13 @@ def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True):
     bf16 = dtype == torch.bfloat16
     do = randn((n, heads, dim), dtype, seed + 3) if backward else None
     do64 = np64(do) if backward else None
-    terms = attn_abs_terms(q64, k64, v64, do64, ref_lse, off, causal) if bf16 else None
+    terms = None
+    if bf16:  # rounding bounds on the repeated-head problem; dK / dV bounds summed per group
+        g = heads // kv_heads
+        terms = list(attn_abs_terms(q64, np.repeat(k64, g, axis=1), np.repeat(v64, g, axis=1),
+                                    do64, ref_lse, off, causal))
+        if backward:
+            terms[1], terms[3] = _fold(terms[1], kv_heads), _fold(terms[3], kv_heads)
     check_close("O", np64(out), ref_o, 2e-3,
                 extra=(2 * terms[0] + np.abs(ref_o)) if bf16 else None, unit=u)
     check_close("LSE", lse.cpu().numpy().astype(np.float64), ref_lse, 1e-4 + 1e-5 * np.abs(ref_lse).max())
@@ -56,6 +68,46 @@ def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True):
 @pytest.mark.parametrize("causal", [True, False])
 def test_edge_lengths(dim, dtype, causal):
     _run_case(EDGE_LENGTHS, 2, dim, dtype, causal, seed=dim)
+
+
+@pytest.mark.parametrize("dim", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_grouped_query_edge_lengths(dim, dtype, causal):
+    """Grouped-query attention: 8 query heads on 2 K/V heads (groups of 4)."""
+    _run_case(EDGE_LENGTHS, 8, dim, dtype, causal, seed=100 + dim, kv_heads=2)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(4, 1), (6, 3), (16, 8), (32, 4)])
+def test_grouped_query_head_ratios(heads, kv_heads):
+    """Group sizes 4, 2, 2, 8 (the last two with heads a multiple of 8, where the
+    grid keeps each group on one XCD)."""
+    _run_case([300, 17, 129, 640], heads, 64, torch.float16, True, seed=heads + kv_heads,
+              kv_heads=kv_heads)
+
+
+def test_grouped_query_autograd_matches_launchers():
+    """The autograd path gives the launchers' dq / dk / dv bit for bit (GQA)."""
+    from scree_amd.kernels.hip import (varlen_attention_hip, varlen_attention_hip_autograd,
+                                       varlen_attention_hip_backward)
+
+    lengths = [200, 1, 77, 512]
+    say(f"case: gqa autograd lengths={lengths} H=8 Hkv=2 D=64 fp16")
+    off, cu = cu_of(lengths)
+    n = sum(lengths)
+    q = randn((n, 8, 64), torch.float16, 7)
+    k = randn((n, 2, 64), torch.float16, 8)
+    v = randn((n, 2, 64), torch.float16, 9)
+    do = randn((n, 8, 64), torch.float16, 10)
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = varlen_attention_hip_autograd(qa, ka, va, cu, causal=True)
+    out.backward(do)
+    o2, lse = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    dq, dk, dv = varlen_attention_hip_backward(do, q, k, v, o2, lse, cu, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.detach(), o2)
+    assert torch.equal(qa.grad, dq) and torch.equal(ka.grad, dk) and torch.equal(va.grad, dv)
+    assert ka.grad.shape == (n, 2, 64)
 
 
 def test_single_token_sequences():

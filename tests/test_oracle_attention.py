@@ -212,3 +212,79 @@ def test_empty_sequence_is_skipped():
     o2, lse2 = attention_fwd(q, k, v, offsets_from_lengths([3, 2]), causal=True)
     np.testing.assert_array_equal(o, o2)
     np.testing.assert_array_equal(lse, lse2)
+
+
+# ----------------------------------------------------------- grouped-query
+def _sdpa_gqa(q, k, v, off, causal, want_grad=False, do=None):
+    """torch SDPA with enable_gqa per sequence (fp64 CPU), and its autograd."""
+    qt, kt, vt = (torch.tensor(a, requires_grad=want_grad) for a in (q, k, v))
+    outs = []
+    for b in range(len(off) - 1):
+        s, e = int(off[b]), int(off[b + 1])
+        if e <= s:
+            continue
+        o = F.scaled_dot_product_attention(qt[s:e].transpose(0, 1)[None], kt[s:e].transpose(0, 1)[None],
+                                           vt[s:e].transpose(0, 1)[None], is_causal=causal,
+                                           enable_gqa=True)
+        outs.append(o[0].transpose(0, 1))
+    out = torch.cat(outs)
+    if not want_grad:
+        return out.detach().numpy()
+    out.backward(torch.tensor(do))
+    return out.detach().numpy(), qt.grad.numpy(), kt.grad.numpy(), vt.grad.numpy()
+
+
+@pytest.mark.parametrize("kv_heads", [1, 2, 3])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_forward_and_backward_match_sdpa(kv_heads, causal):
+    lengths = [5, 1, 9, 3]
+    rng = np.random.default_rng(kv_heads)
+    n, h, d = sum(lengths), 6, 8
+    off = offsets_from_lengths(lengths)
+    q = rng.standard_normal((n, h, d))
+    k = rng.standard_normal((n, kv_heads, d))
+    v = rng.standard_normal((n, kv_heads, d))
+    do = rng.standard_normal((n, h, d))
+    o, lse = attention_fwd(q, k, v, off, causal=causal)
+    want_o, wdq, wdk, wdv = _sdpa_gqa(q, k, v, off, causal, want_grad=True, do=do)
+    np.testing.assert_allclose(o, want_o, atol=1e-12)
+    np.testing.assert_allclose(lse, attention_lse(q, k, off, causal=causal), atol=1e-12)
+    dq, dk, dv, _ = attention_bwd(do, q, k, v, o, lse, off, causal=causal)
+    assert dk.shape == k.shape and dv.shape == v.shape
+    np.testing.assert_allclose(dq, wdq, atol=1e-10)
+    np.testing.assert_allclose(dk, wdk, atol=1e-10)
+    np.testing.assert_allclose(dv, wdv, atol=1e-10)
+
+
+def test_gqa_single_kv_head_gives_identical_query_heads():
+    """With one K/V head, query heads holding the same queries see the same keys."""
+    rng = np.random.default_rng(11)
+    lengths = [7, 4]
+    n, d = sum(lengths), 4
+    off = offsets_from_lengths(lengths)
+    q1 = rng.standard_normal((n, 1, d))
+    q = np.repeat(q1, 3, axis=1)
+    k = rng.standard_normal((n, 1, d))
+    v = rng.standard_normal((n, 1, d))
+    o, lse = attention_fwd(q, k, v, off, causal=True)
+    o1, lse1 = attention_fwd(q1, k, v, off, causal=True)
+    for hh in range(3):
+        np.testing.assert_allclose(o[:, hh], o1[:, 0], atol=1e-13)
+        np.testing.assert_allclose(lse[:, hh], lse1[:, 0], atol=1e-13)
+    do = rng.standard_normal((n, 3, d))
+    dq, dk, dv, _ = attention_bwd(do, q, k, v, o, lse, off, causal=True)
+    # dK / dV of the shared head = sum of the three single-head gradients
+    acc_k, acc_v = np.zeros_like(k), np.zeros_like(v)
+    for hh in range(3):
+        _, dk1, dv1, _ = attention_bwd(do[:, hh:hh + 1], q1, k, v, o1, lse1, off, causal=True)
+        acc_k += dk1
+        acc_v += dv1
+    np.testing.assert_allclose(dk, acc_k, atol=1e-12)
+    np.testing.assert_allclose(dv, acc_v, atol=1e-12)
+
+
+def test_gqa_rejects_non_dividing_heads():
+    q = np.zeros((3, 4, 8))
+    k = np.zeros((3, 3, 8))
+    with pytest.raises(ValueError):
+        attention_fwd(q, k, k, np.array([0, 3]))
