@@ -11,10 +11,12 @@ pass into preallocated buffers.  ``value`` is real-token causal TFLOP/s
 (4*H*D*sum L(L+1)/2 forward, x3.5 for forward+backward).
 
 Also reported (``secondary``): config 3 forward, config 4 on the reference's
-fixed H100 length list, config 5 (bf16, 32x128) forward+backward, config 2
-RMSNorm / LayerNorm forward and backward GB/s, varlen softmax forward and
-backward and packed <-> padded conversions GB/s at the config-2 shape, the
-user-facing autograd step,
+fixed H100 length list, config 4 with grouped-query attention (16 query heads
+on 4 K/V heads), config 5 (bf16, 32x128) forward+backward, config 2
+RMSNorm / LayerNorm / fused add + RMSNorm forward and backward GB/s, varlen
+softmax forward and backward and packed <-> padded conversions GB/s at the
+config-2 shape, torch's own SDPA on the same GPU for calibration (uniform
+lengths with cfg4's token count), the user-facing autograd step,
 and per-kernel HIP-event timings.  ``roofline`` describes the dominant kernel
 of the primary step; ``cpu_baseline`` times the numpy oracle (the reference's
 einsum call pattern) on a bounded sample of the same workload.
@@ -59,7 +61,7 @@ def _events_time(fn, reps: int) -> float:
 class AttnCase:
     """Preallocated tensors and the four launches of one attention step."""
 
-    def __init__(self, cfg, dtype, seed=0):
+    def __init__(self, cfg, dtype, seed=0, kv_heads=None):
         import numpy as np
         import torch
 
@@ -68,15 +70,16 @@ class AttnCase:
         self.cfg, self.A = cfg, A
         dev = torch.device("cuda:0")
         n, h, d = cfg.total, cfg.heads, cfg.head_dim
+        hk = h if kv_heads is None else kv_heads  # grouped-query: fewer K/V heads
         g = torch.Generator(device=dev).manual_seed(seed)
-        self.q, self.k, self.v, self.do = (torch.randn(n, h, d, device=dev, dtype=dtype, generator=g)
-                                           for _ in range(4))
+        self.q, self.k, self.v, self.do = (torch.randn(n, hh, d, device=dev, dtype=dtype, generator=g)
+                                           for hh in (h, hk, hk, h))
         off = np.zeros(len(cfg.lengths) + 1, dtype=np.int32)
         off[1:] = np.cumsum(cfg.lengths)
         self.cu = torch.from_numpy(off).to(dev)
         self.out = torch.empty_like(self.q)
         self.lse = torch.empty(n, h, device=dev, dtype=torch.float32)
-        self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
+        self.dq, self.dk, self.dv = (torch.empty_like(t) for t in (self.q, self.k, self.v))
         self.delta = torch.empty(n, h, device=dev, dtype=torch.float32)
         self.ws = torch.empty(A.workspace_bytes(len(cfg.lengths), n, d), dtype=torch.uint8, device=dev)
 
@@ -105,10 +108,10 @@ class AttnCase:
         self.bwd_dkv()
 
 
-def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False):
+def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False, kv_heads=None):
     import torch
 
-    case = AttnCase(cfg, dtype)
+    case = AttnCase(cfg, dtype, kv_heads=kv_heads)
     step = case.step_fwd_bwd if backward else case.step_fwd
     for _ in range(warmup):
         step()
@@ -157,6 +160,17 @@ def time_norms(cfg, steps, warmup):
         "layernorm_fwd": (lambda: Nm.layernorm_fwd(x, w, b, cfg.eps, True), lfb),
         "layernorm_bwd": (lambda: Nm.layernorm_bwd(dy, x, w, mean, lrstd, True, True, p_like=w), lbb),
     }
+    # fused residual add + RMSNorm: reads x, r (and w), writes h, y; backward
+    # reads dy, dh, h (and w), writes dx (and dw)
+    r = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+    dh = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+    h, _, hrstd = Nm.add_rmsnorm_fwd(x, r, w, cfg.eps, True)
+    afb = 4.0 * 2 * rows * dim + 2 * dim
+    abb = 4.0 * 2 * rows * dim + 2 * 2 * dim
+    cases["add_rmsnorm_fwd"] = (lambda: Nm.add_rmsnorm_fwd(x, r, w, cfg.eps, True), afb)
+    cases["add_rmsnorm_bwd"] = (lambda: Nm.add_rmsnorm_bwd(dy, dh, h, w, hrstd, True, dw_like=w), abb)
+    # the two steps it replaces (torch add, then this library's RMSNorm), same algorithmic bytes
+    cases["unfused_add_then_rmsnorm_fwd"] = (lambda: Nm.rmsnorm_fwd(x + r, w, cfg.eps, True), afb)
     y = torch.empty_like(x)
     cases["device_copy_same_bytes"] = (lambda: y.copy_(x), 2.0 * x.numel() * x.element_size())
     # varlen softmax along the ragged axis at the same shape (x: 19758 x 4096 bf16)
@@ -188,6 +202,31 @@ def time_norms(cfg, steps, warmup):
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"ms": ms, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS, "bytes": nbytes}
     return out
+
+
+def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup):
+    """Calibration: torch's own fused attention (default SDPA dispatch) on a
+    uniform-length batch with the same tokens, causal fp16, forward + backward."""
+    import torch
+    import torch.nn.functional as F
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    shape = (batch, heads, seqlen, head_dim)
+    q, k, v, do = (torch.randn(*shape, device=dev, dtype=torch.float16, generator=g) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def step():
+        o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        o.backward(do)
+
+    for _ in range(warmup):
+        step()
+    ms = _events_time(step, steps)
+    from scree_amd.workloads import attn_fwd_flops
+    flops = 3.5 * attn_fwd_flops([seqlen] * batch, heads, head_dim, True)
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
 def time_autograd_step(cfg, dtype, steps, warmup):
@@ -378,6 +417,23 @@ def main() -> int:
                                           "mfma_frac": round(r["mfma_frac"], 4),
                                           "kernels_us": {k: round(v * 1e3, 1) for k, v in r["kernels_ms"].items()}}
         log(f"cfg5: {r['ms']:.3f} ms {r['tflops']:.1f} TFLOP/s")
+        gq = workloads.config4()
+        gq.name = "cfg4_gqa_16q_4kv"
+        r, _ = time_attention(gq, fp16, args.steps, args.warmup, backward=True, kv_heads=4)
+        secondary["cfg4_gqa_16q_heads_4kv_heads"] = {"ms": round(r["ms"], 4),
+                                                      "tflops": round(r["tflops"], 2),
+                                                      "mfma_frac": round(r["mfma_frac"], 4)}
+        log(f"cfg4 GQA 16q/4kv: {r['ms']:.4f} ms {r['tflops']:.1f} TFLOP/s")
+        uni = workloads.AttnConfig("uniform_16x760_fp16_16x64", [760] * 16, 16, 64, "fp16", True, True)
+        ours, _ = time_attention(uni, fp16, args.steps, args.warmup, backward=True)
+        ref = time_sdpa_reference(16, 64, 16, 760, args.steps, args.warmup)
+        secondary["vendor_calibration_uniform_16x760"] = {
+            "what": "causal fp16 fwd+bwd, 16 seqs x 760 tokens (12160, as cfg4), 16x64: this "
+                    "library's step vs torch.nn.functional.scaled_dot_product_attention (default "
+                    "ROCm dispatch, padded batch of equal lengths) on the same GPU",
+            "ours_ms": round(ours["ms"], 4), "ours_tflops": round(ours["tflops"], 2),
+            "torch_sdpa_ms": round(ref["ms"], 4), "torch_sdpa_tflops": round(ref["tflops"], 2)}
+        log(f"calibration 16x760: ours {ours['tflops']:.0f} TF/s, torch SDPA {ref['tflops']:.0f} TF/s")
         nr = time_norms(workloads.config2(), args.steps, args.warmup)
         secondary["cfg2_norms_bf16"] = {k: {"us": round(v["ms"] * 1e3, 2), "GB/s": round(v["GB/s"], 1),
                                             "hbm_frac": round(v["hbm_frac"], 4)} for k, v in nr.items()}

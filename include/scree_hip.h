@@ -188,6 +188,27 @@ int scree_layernorm_bwd(const void* dy, const void* x, const void* weight, const
                         int dparam_dtype, int64_t rows, int64_t dim, int dtype,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Fused residual add + RMSNorm, the pre-norm transformer step
+ *   h = x + residual;  y = rmsnorm(h) [* weight]
+ * of the reference's block (examples/03_train_step.py:46-48: h1 = x +
+ * attn_proj, then varlen_rmsnorm(h1)) in one pass: h is x + residual rounded
+ * to `dtype` exactly as the separate addition rounds it, and y is
+ * scree_rmsnorm_fwd of that h, bit for bit.  h and y must not alias x or
+ * residual.  No fused counterpart in the reference. */
+int scree_add_rmsnorm_fwd(const void* x, const void* residual, const void* weight, void* h,
+                          void* y, float* rstd, int64_t rows, int64_t dim, float eps, int dtype,
+                          void* stream);
+
+/* Backward of scree_add_rmsnorm_fwd: dx (the gradient of both x and residual)
+ * = dh + the RMSNorm input gradient of dy at h, and dweight as in
+ * scree_rmsnorm_bwd.  dh, the gradient reaching h by the residual stream, may
+ * be NULL (then dx is scree_rmsnorm_bwd's dx).  `workspace` as for
+ * scree_rmsnorm_bwd (scree_norm_bwd_workspace_bytes). */
+int scree_add_rmsnorm_bwd(const void* dy, const void* dh, const void* h, const void* weight,
+                          const float* rstd, void* dx, void* dweight, int dparam_dtype,
+                          int64_t rows, int64_t dim, int dtype, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ softmax
  * Replaces scree.kernels.reference.varlen_softmax
  * (src/scree/kernels/reference/varlen_softmax.py:13-63), whose torch branch

@@ -30,6 +30,12 @@ Pinning status of every function (how a plausible mistake would be caught):
   ``F.layer_norm``, unit-RMS and zero-mean/unit-variance properties.
 * ``norms.*_bwd`` -- torch autograd of ``F.rms_norm`` / ``F.layer_norm`` and
   fp64 finite differences.
+* ``norms.round_bf16`` / ``norms.add_rounded`` -- torch's own float32 ->
+  bfloat16 conversion and half-precision ``x + r`` on the CPU, bit for bit,
+  including ties and values near the rounding boundary.
+* ``norms.add_rmsnorm_fwd`` / ``norms.add_rmsnorm_bwd`` -- torch autograd of
+  ``h = x + r; F.rms_norm(h)`` in fp64 with gradients arriving at both ``h``
+  and ``y``; the unfused composition ``rmsnorm_fwd(add_rounded(...))``.
 * ``softmax.varlen_softmax`` -- the reference's two known-answer tests
   (``tests/test_varlen_kernels.py:119-139``: per-sequence rows sum to one,
   per-sequence numpy baseline), ``torch.softmax`` per sequence, and the

@@ -83,3 +83,55 @@ def layernorm_bwd(dy, x, weight=None, eps=1e-5, has_bias=False, dtype=np.float64
     dw = (dy * xhat).reshape(-1, d).sum(axis=0) if weight is not None else None
     db = dy.reshape(-1, d).sum(axis=0) if has_bias else None
     return dx, dw, db
+
+
+# ----------------------------------------------------- fused add + RMSNorm
+# No counterpart in the reference: its transformer block adds the attention
+# output to the residual stream and then normalises
+# (``examples/03_train_step.py:46-48``).  The fused form returns both the sum
+# ``h`` and ``y = rmsnorm(h)``; ``h`` is rounded to the storage dtype the way
+# the separate half-precision addition rounds it (operands widened to fp32,
+# summed in fp32, the fp32 sum rounded to nearest-even), and ``y`` is RMSNorm
+# of that rounded ``h``.
+
+def round_bf16(x):
+    """Round to bfloat16 (nearest, ties to even) and return float64.
+
+    Standard bit-level method on the fp32 pattern: add ``0x7fff`` plus the
+    lowest kept bit, then clear the low 16 bits.  Inputs are first rounded to
+    fp32 (numpy has no bfloat16); NaN is not expected here.
+    """
+    f = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def add_rounded(x, residual, storage="float64"):
+    """``x + residual`` as a ``storage``-dtype tensor addition produces it."""
+    if storage == "float64":
+        return np.asarray(x, dtype=np.float64) + np.asarray(residual, dtype=np.float64)
+    s32 = np.asarray(x, dtype=np.float32) + np.asarray(residual, dtype=np.float32)
+    if storage == "float32":
+        return s32.astype(np.float64)
+    if storage == "float16":
+        return s32.astype(np.float16).astype(np.float64)
+    if storage == "bfloat16":
+        return round_bf16(s32)
+    raise ValueError(f"unknown storage dtype {storage}")
+
+
+def add_rmsnorm_fwd(x, residual, weight=None, eps=1e-6, storage="float64", dtype=np.float64):
+    """Return ``(h, y, rstd)``: ``h = x + residual`` (rounded as ``storage``), ``y = rmsnorm(h)``."""
+    h = add_rounded(x, residual, storage)
+    y, rstd = rmsnorm_fwd(h, weight, eps, dtype)
+    return h, y, rstd
+
+
+def add_rmsnorm_bwd(dy, dh, h, weight=None, eps=1e-6, dtype=np.float64):
+    """Return ``(dx, dweight)``: ``dx = dh + dRMSNorm(dy)`` at ``h`` is the
+    gradient of both ``x`` and ``residual``; ``dh`` may be None."""
+    dx, dw = rmsnorm_bwd(dy, h, weight, eps, dtype)
+    if dh is not None:
+        dx = dx + np.asarray(dh, dtype=dtype)
+    return dx, dw

@@ -29,9 +29,12 @@ constexpr int kMaxParts = 512;     // partial rows of a backward, at most
 constexpr int kMaxChunks = 16;     // 16-byte vectors per lane on the fast path
 
 // ------------------------------------------------------------------ forward
-template <typename T, int CHUNKS, bool LAYER>
+// RES (RMSNorm only): the normalised row is h = x + res, rounded to T as a
+// separate addition would round it; h is written out and normalised.
+template <typename T, int CHUNKS, bool LAYER, bool RES>
 __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
-    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ b, T* __restrict__ y,
+    const T* __restrict__ x, const T* __restrict__ res, const T* __restrict__ w,
+    const T* __restrict__ b, T* __restrict__ hout, T* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows, int dim, float eps) {
   constexpr int VEC = 16 / sizeof(T);
   const int lane = threadIdx.x & (kWave - 1);
@@ -44,6 +47,22 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
   for (int c = 0; c < CHUNKS; ++c) {
     const int vi = c * kWave + lane;
     v[c] = vi < nvec ? ld16_nt(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+  }
+  if (RES) {
+    const T* rr = res + row * (int64_t)dim;
+    T* hr = hout + row * (int64_t)dim;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int vi = c * kWave + lane;
+      if (vi < nvec) {
+        const uint4 rv = ld16_nt(rr + (int64_t)vi * VEC);
+        float f[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) f[e] = elem<T>(v[c], e) + elem<T>(rv, e);
+        v[c] = pack16<T>(f);
+        st16_nt(hr + (int64_t)vi * VEC, v[c]);
+      }
+    }
   }
   const float fdim = (float)dim;
   float mu = 0.f, rstd;
@@ -102,37 +121,47 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
   }
 }
 
-template <typename T, bool LAYER>
+template <typename T, bool LAYER, bool RES>
 __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_generic(
-    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ b, T* __restrict__ y,
+    const T* __restrict__ x, const T* __restrict__ res, const T* __restrict__ w,
+    const T* __restrict__ b, T* __restrict__ hout, T* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows, int dim, float eps) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x / kWave);
   if (row >= rows) return;
   const T* xr = x + row * (int64_t)dim;
+  const T* rr = RES ? res + row * (int64_t)dim : nullptr;
+  // Element j of the normalised row: x, or h = x + res rounded to T (each
+  // pass recomputes it rather than reading back the h it stores).
+  auto at = [&](int j) -> float {
+    return RES ? to_f32(from_f32<T>(to_f32(xr[j]) + to_f32(rr[j]))) : to_f32(xr[j]);
+  };
   const float fdim = (float)dim;
   float mu = 0.f, rstd;
   if (LAYER) {
     float s = 0.f;
-    for (int j = lane; j < dim; j += kWave) s += to_f32(xr[j]);
+    for (int j = lane; j < dim; j += kWave) s += at(j);
     mu = wave_sum(s) / fdim;
     float s2 = 0.f;
     for (int j = lane; j < dim; j += kWave) {
-      const float d = to_f32(xr[j]) - mu;
+      const float d = at(j) - mu;
       s2 += d * d;
     }
     rstd = 1.0f / sqrtf(wave_sum(s2) / fdim + eps);
   } else {
     float s = 0.f;
     for (int j = lane; j < dim; j += kWave) {
-      const float t = to_f32(xr[j]);
+      const float t = at(j);
       s += t * t;
     }
     rstd = 1.0f / sqrtf(wave_sum(s) / fdim + eps);
   }
   T* yr = y + row * (int64_t)dim;
+  T* hr = RES ? hout + row * (int64_t)dim : nullptr;
   for (int j = lane; j < dim; j += kWave) {
-    float t = LAYER ? (to_f32(xr[j]) - mu) * rstd : to_f32(xr[j]) * rstd;
+    const float hj = at(j);
+    if (RES) hr[j] = from_f32<T>(hj);
+    float t = LAYER ? (hj - mu) * rstd : hj * rstd;
     if (w) t *= to_f32(w[j]);
     if (LAYER && b) t += to_f32(b[j]);
     yr[j] = from_f32<T>(t);
@@ -158,11 +187,14 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_generic(
 constexpr int kBwdThreads = 512;
 constexpr int kBwdWarps = kBwdThreads / kWave;
 
-template <typename T, int CPT, int R, bool LAYER>
+// RES: dx also receives dres (the gradient reaching the normalised input by
+// another path, e.g. the residual stream of an add + RMSNorm).
+template <typename T, int CPT, int R, bool LAYER, bool RES>
 __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
-    const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ dx,
-    float* __restrict__ partial, int64_t rows, int dim, int nparam, int64_t rows_per_block) {
+    const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+    const T* __restrict__ dres, T* __restrict__ dx, float* __restrict__ partial, int64_t rows,
+    int dim, int nparam, int64_t rows_per_block) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float red[2][R][2][kBwdWarps];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -190,7 +222,7 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
 
   int buf = 0;
   for (int64_t rb = r0; rb < r1; rb += R) {
-    uint4 xv[R][CPT], gv[R][CPT];
+    uint4 xv[R][CPT], gv[R][CPT], hv[RES ? R : 1][CPT];
     float rs[R], mu[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -203,6 +235,7 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
         const int64_t off = row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC;
         xv[r][k] = (ok && own[k]) ? ld16_nt(x + off) : make_uint4(0, 0, 0, 0);
         gv[r][k] = (ok && own[k]) ? ld16_nt(dy + off) : make_uint4(0, 0, 0, 0);
+        if (RES) hv[r][k] = (ok && own[k]) ? ld16_nt(dres + off) : make_uint4(0, 0, 0, 0);
       }
     }
     float s1[R], s2[R];
@@ -243,6 +276,9 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
       for (int k = 0; k < CPT; ++k) {
         asm volatile("" : "+v"(xv[r][k].x), "+v"(xv[r][k].y), "+v"(xv[r][k].z), "+v"(xv[r][k].w));
         asm volatile("" : "+v"(gv[r][k].x), "+v"(gv[r][k].y), "+v"(gv[r][k].z), "+v"(gv[r][k].w));
+        if (RES)
+          asm volatile("" : "+v"(hv[RES ? r : 0][k].x), "+v"(hv[RES ? r : 0][k].y),
+                       "+v"(hv[RES ? r : 0][k].z), "+v"(hv[RES ? r : 0][k].w));
       }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -274,6 +310,7 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
             f[e] = rs[r] * g - k_rms * xx;
             aw[k][e] += d * xx * rs[r];
           }
+          if (RES) f[e] += elem<T>(hv[RES ? r : 0][k], e);
         }
         st16_nt(dx + row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC, pack16<T>(f));
       }
@@ -295,11 +332,11 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
   }
 }
 
-template <typename T, bool LAYER>
+template <typename T, bool LAYER, bool RES>
 __global__ __launch_bounds__(kFwdWaves* kWave) void norm_bwd_dx_generic(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
-    const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ dx,
-    int64_t rows, int dim) {
+    const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+    const T* __restrict__ dres, T* __restrict__ dx, int64_t rows, int dim) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x / kWave);
   if (row >= rows) return;
@@ -330,7 +367,8 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_bwd_dx_generic(
     const float xx = to_f32(xr[j]);
     const float d = to_f32(gr[j]);
     const float g = w ? d * to_f32(w[j]) : d;
-    const float v = LAYER ? r * (g - a_ln - ((xx - mu) * r) * b_ln) : r * g - k_rms * xx;
+    float v = LAYER ? r * (g - a_ln - ((xx - mu) * r) * b_ln) : r * g - k_rms * xx;
+    if (RES) v += to_f32(dres[row * (int64_t)dim + j]);
     dxr[j] = from_f32<T>(v);
   }
 }
@@ -474,22 +512,19 @@ inline int64_t rows_per_part(int64_t rows, int nparts) {
   return ((r + 7) / 8) * 8;
 }
 
-template <typename T, bool LAYER>
-int launch_fwd(const void* x, const void* w, const void* b, void* y, float* mean, float* rstd,
-               int64_t rows, int64_t dim, float eps, hipStream_t stream) {
+// res / h non-null (RMSNorm only): normalise h = x + res and write h too.
+template <typename T, bool LAYER, bool RES>
+void launch_fwd_k(const T* xp, const T* rp, const T* wp, const T* bp, T* hp, T* yp, float* mean,
+                  float* rstd, int64_t rows, int64_t dim, float eps, hipStream_t stream) {
   const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
   const dim3 block(kFwdWaves * kWave);
-  const T* xp = static_cast<const T*>(x);
-  const T* wp = static_cast<const T*>(w);
-  const T* bp = static_cast<const T*>(b);
-  T* yp = static_cast<T*>(y);
   const int d = (int)dim;
-  if (fast_path_ok<T>(dim, {x, w, b, y})) {
+  if (fast_path_ok<T>(dim, {xp, rp, wp, bp, hp, yp})) {
     const int chunks = chunks_for((int)(dim / (16 / sizeof(T))));
-#define SCREE_FWD_CASE(C)                                                                        \
-  case C:                                                                                        \
-    hipLaunchKernelGGL((norm_fwd_vec<T, C, LAYER>), grid, block, 0, stream, xp, wp, bp, yp, mean, \
-                       rstd, rows, d, eps);                                                      \
+#define SCREE_FWD_CASE(C)                                                                      \
+  case C:                                                                                      \
+    hipLaunchKernelGGL((norm_fwd_vec<T, C, LAYER, RES>), grid, block, 0, stream, xp, rp, wp, bp, \
+                       hp, yp, mean, rstd, rows, d, eps);                                      \
     break;
     switch (chunks) {
       SCREE_FWD_CASE(1)
@@ -497,57 +532,99 @@ int launch_fwd(const void* x, const void* w, const void* b, void* y, float* mean
       SCREE_FWD_CASE(4)
       SCREE_FWD_CASE(8)
       SCREE_FWD_CASE(16)
-      default:
-        return set_error(SCREE_ERR_INVALID, "norm forward: internal chunk count %d", chunks);
+      default: break;  // chunks_for never exceeds kMaxChunks on the fast path
     }
 #undef SCREE_FWD_CASE
   } else {
-    hipLaunchKernelGGL((norm_fwd_generic<T, LAYER>), grid, block, 0, stream, xp, wp, bp, yp, mean,
-                       rstd, rows, d, eps);
+    hipLaunchKernelGGL((norm_fwd_generic<T, LAYER, RES>), grid, block, 0, stream, xp, rp, wp, bp,
+                       hp, yp, mean, rstd, rows, d, eps);
   }
-  return check_launch(LAYER ? "scree_layernorm_fwd" : "scree_rmsnorm_fwd");
 }
 
 template <typename T, bool LAYER>
-int launch_bwd(const void* dy, const void* x, const void* w, const float* mean, const float* rstd,
-               void* dx, void* dw, void* db, int dparam_dtype, int64_t rows, int64_t dim,
-               void* workspace, hipStream_t stream) {
-  const T* dyp = static_cast<const T*>(dy);
+int launch_fwd(const void* x, const void* res, const void* w, const void* b, void* h, void* y,
+               float* mean, float* rstd, int64_t rows, int64_t dim, float eps,
+               hipStream_t stream) {
   const T* xp = static_cast<const T*>(x);
+  const T* rp = static_cast<const T*>(res);
   const T* wp = static_cast<const T*>(w);
-  T* dxp = static_cast<T*>(dx);
+  const T* bp = static_cast<const T*>(b);
+  T* hp = static_cast<T*>(h);
+  T* yp = static_cast<T*>(y);
+  if constexpr (!LAYER) {
+    if (res) {
+      launch_fwd_k<T, false, true>(xp, rp, wp, bp, hp, yp, mean, rstd, rows, dim, eps, stream);
+      return check_launch("scree_add_rmsnorm_fwd");
+    }
+  }
+  launch_fwd_k<T, LAYER, false>(xp, nullptr, wp, bp, nullptr, yp, mean, rstd, rows, dim, eps,
+                                stream);
+  return check_launch(LAYER ? "scree_layernorm_fwd" : "scree_rmsnorm_fwd");
+}
+
+// dres non-null (RMSNorm only): dx also receives dres.
+template <typename T, bool LAYER, bool RES>
+void launch_bwd_k(const T* dyp, const T* xp, const T* wp, const float* mean, const float* rstd,
+                  const T* dresp, T* dxp, float* partial, bool want_params, int nparts,
+                  int64_t rows, int64_t dim, hipStream_t stream) {
   const int d = (int)dim;
   const int nparam = LAYER ? 2 : 1;
-  const bool want_params = (dw != nullptr) || (db != nullptr);
-  const int nparts = nparts_for(rows);
-  float* partial = static_cast<float*>(workspace);
-  if (bwd_fast_path_ok<T>(dim, {dy, x, w, dx})) {
+  if (bwd_fast_path_ok<T>(dim, {dyp, xp, wp, dresp, dxp})) {
     const int nvec = (int)(dim / (16 / sizeof(T)));
     const int cpt = (nvec + kBwdThreads - 1) / kBwdThreads;  // 1 or 2
     const int64_t rpb = rows_per_part(rows, nparts);
     const dim3 grid((unsigned)nparts), block(kBwdThreads);
     const int np = want_params ? nparam : 0;
-    // rows per step: as many as fit 4 waves per SIMD (LN keeps two sums per row)
-    constexpr int R1 = LAYER ? 4 : 8;
-    constexpr int R2 = LAYER ? 2 : 4;
+    // rows per step: as many as fit 4 waves per SIMD (LN keeps two sums per
+    // row; the residual gradient is one more vector per row)
+    constexpr int R1 = (LAYER || RES) ? 4 : 8;
+    constexpr int R2 = (LAYER || RES) ? 2 : 4;
     if (cpt == 1)
-      hipLaunchKernelGGL((norm_bwd_cols<T, 1, R1, LAYER>), grid, block, 0, stream, dyp, xp, wp, mean,
-                         rstd, dxp, partial, rows, d, np, rpb);
+      hipLaunchKernelGGL((norm_bwd_cols<T, 1, R1, LAYER, RES>), grid, block, 0, stream, dyp, xp, wp,
+                         mean, rstd, dresp, dxp, partial, rows, d, np, rpb);
     else
-      hipLaunchKernelGGL((norm_bwd_cols<T, 2, R2, LAYER>), grid, block, 0, stream, dyp, xp, wp, mean,
-                         rstd, dxp, partial, rows, d, np, rpb);
+      hipLaunchKernelGGL((norm_bwd_cols<T, 2, R2, LAYER, RES>), grid, block, 0, stream, dyp, xp, wp,
+                         mean, rstd, dresp, dxp, partial, rows, d, np, rpb);
   } else {
     const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves)), block(kFwdWaves * kWave);
     if (rows > 0)
-      hipLaunchKernelGGL((norm_bwd_dx_generic<T, LAYER>), grid, block, 0, stream, dyp, xp, wp,
-                         mean, rstd, dxp, rows, d);
+      hipLaunchKernelGGL((norm_bwd_dx_generic<T, LAYER, RES>), grid, block, 0, stream, dyp, xp, wp,
+                         mean, rstd, dresp, dxp, rows, d);
     if (want_params) {
       const dim3 pgrid((unsigned)((dim + 255) / 256), (unsigned)nparts);
       hipLaunchKernelGGL((norm_bwd_param_generic<T, LAYER>), pgrid, dim3(256), 0, stream, dyp, xp,
                          mean, rstd, partial, rows, d, nparam);
     }
   }
-  int rc = check_launch(LAYER ? "scree_layernorm_bwd" : "scree_rmsnorm_bwd");
+}
+
+template <typename T, bool LAYER>
+int launch_bwd(const void* dy, const void* x, const void* w, const float* mean, const float* rstd,
+               const void* dres, void* dx, void* dw, void* db, int dparam_dtype, int64_t rows,
+               int64_t dim, void* workspace, hipStream_t stream) {
+  const T* dyp = static_cast<const T*>(dy);
+  const T* xp = static_cast<const T*>(x);
+  const T* wp = static_cast<const T*>(w);
+  const T* dresp = static_cast<const T*>(dres);
+  T* dxp = static_cast<T*>(dx);
+  const int d = (int)dim;
+  const int nparam = LAYER ? 2 : 1;
+  const bool want_params = (dw != nullptr) || (db != nullptr);
+  const int nparts = nparts_for(rows);
+  float* partial = static_cast<float*>(workspace);
+  const char* fn = LAYER ? "scree_layernorm_bwd" : (dres ? "scree_add_rmsnorm_bwd" : "scree_rmsnorm_bwd");
+  bool done = false;
+  if constexpr (!LAYER) {
+    if (dres) {
+      launch_bwd_k<T, false, true>(dyp, xp, wp, mean, rstd, dresp, dxp, partial, want_params,
+                                   nparts, rows, dim, stream);
+      done = true;
+    }
+  }
+  if (!done)
+    launch_bwd_k<T, LAYER, false>(dyp, xp, wp, mean, rstd, nullptr, dxp, partial, want_params,
+                                  nparts, rows, dim, stream);
+  int rc = check_launch(fn);
   if (rc != SCREE_OK || !want_params) return rc;
   if (dim % 4 == 0) {
     const dim3 cgrid((unsigned)((dim + 15) / 16), (unsigned)nparam);
@@ -558,7 +635,7 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* mean, 
     hipLaunchKernelGGL(norm_param_colsum, cgrid, dim3(256), 0, stream, partial, nparts, nparam, d,
                        dw, db, dparam_dtype);
   }
-  return check_launch(LAYER ? "scree_layernorm_bwd (param sum)" : "scree_rmsnorm_bwd (param sum)");
+  return check_launch(fn);
 }
 
 int validate_common(const char* fn, int64_t rows, int64_t dim, int dtype) {
@@ -592,9 +669,9 @@ extern "C" int scree_rmsnorm_fwd(const void* x, const void* weight, void* y, flo
   if (!x || !y) return set_error(SCREE_ERR_INVALID, "%s: x and y must be non-null", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case SCREE_DTYPE_F32: return launch_fwd<float, false>(x, weight, nullptr, y, nullptr, rstd, rows, dim, eps, s);
-    case SCREE_DTYPE_F16: return launch_fwd<f16, false>(x, weight, nullptr, y, nullptr, rstd, rows, dim, eps, s);
-    default: return launch_fwd<bf16, false>(x, weight, nullptr, y, nullptr, rstd, rows, dim, eps, s);
+    case SCREE_DTYPE_F32: return launch_fwd<float, false>(x, nullptr, weight, nullptr, nullptr, y, nullptr, rstd, rows, dim, eps, s);
+    case SCREE_DTYPE_F16: return launch_fwd<f16, false>(x, nullptr, weight, nullptr, nullptr, y, nullptr, rstd, rows, dim, eps, s);
+    default: return launch_fwd<bf16, false>(x, nullptr, weight, nullptr, nullptr, y, nullptr, rstd, rows, dim, eps, s);
   }
 }
 
@@ -608,9 +685,9 @@ extern "C" int scree_layernorm_fwd(const void* x, const void* weight, const void
   if (!x || !y) return set_error(SCREE_ERR_INVALID, "%s: x and y must be non-null", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case SCREE_DTYPE_F32: return launch_fwd<float, true>(x, weight, bias, y, mean, rstd, rows, dim, eps, s);
-    case SCREE_DTYPE_F16: return launch_fwd<f16, true>(x, weight, bias, y, mean, rstd, rows, dim, eps, s);
-    default: return launch_fwd<bf16, true>(x, weight, bias, y, mean, rstd, rows, dim, eps, s);
+    case SCREE_DTYPE_F32: return launch_fwd<float, true>(x, nullptr, weight, bias, nullptr, y, mean, rstd, rows, dim, eps, s);
+    case SCREE_DTYPE_F16: return launch_fwd<f16, true>(x, nullptr, weight, bias, nullptr, y, mean, rstd, rows, dim, eps, s);
+    default: return launch_fwd<bf16, true>(x, nullptr, weight, bias, nullptr, y, mean, rstd, rows, dim, eps, s);
   }
 }
 
@@ -645,9 +722,9 @@ extern "C" int scree_rmsnorm_bwd(const void* dy, const void* x, const void* weig
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case SCREE_DTYPE_F32: return launch_bwd<float, false>(dy, x, weight, nullptr, rstd, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
-    case SCREE_DTYPE_F16: return launch_bwd<f16, false>(dy, x, weight, nullptr, rstd, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
-    default: return launch_bwd<bf16, false>(dy, x, weight, nullptr, rstd, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+    case SCREE_DTYPE_F32: return launch_bwd<float, false>(dy, x, weight, nullptr, rstd, nullptr, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+    case SCREE_DTYPE_F16: return launch_bwd<f16, false>(dy, x, weight, nullptr, rstd, nullptr, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+    default: return launch_bwd<bf16, false>(dy, x, weight, nullptr, rstd, nullptr, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
   }
 }
 
@@ -667,8 +744,46 @@ extern "C" int scree_layernorm_bwd(const void* dy, const void* x, const void* we
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case SCREE_DTYPE_F32: return launch_bwd<float, true>(dy, x, weight, mean, rstd, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
-    case SCREE_DTYPE_F16: return launch_bwd<f16, true>(dy, x, weight, mean, rstd, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
-    default: return launch_bwd<bf16, true>(dy, x, weight, mean, rstd, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
+    case SCREE_DTYPE_F32: return launch_bwd<float, true>(dy, x, weight, mean, rstd, nullptr, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
+    case SCREE_DTYPE_F16: return launch_bwd<f16, true>(dy, x, weight, mean, rstd, nullptr, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
+    default: return launch_bwd<bf16, true>(dy, x, weight, mean, rstd, nullptr, dx, dweight, dbias, dparam_dtype, rows, dim, workspace, s);
+  }
+}
+
+extern "C" int scree_add_rmsnorm_fwd(const void* x, const void* residual, const void* weight,
+                                     void* h, void* y, float* rstd, int64_t rows, int64_t dim,
+                                     float eps, int dtype, void* stream) {
+  const char* fn = "scree_add_rmsnorm_fwd";
+  int rc = validate_common(fn, rows, dim, dtype);
+  if (rc) return rc;
+  if (rows == 0) return SCREE_OK;
+  if (!x || !residual || !h || !y)
+    return set_error(SCREE_ERR_INVALID, "%s: x, residual, h and y must be non-null", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32: return launch_fwd<float, false>(x, residual, weight, nullptr, h, y, nullptr, rstd, rows, dim, eps, s);
+    case SCREE_DTYPE_F16: return launch_fwd<f16, false>(x, residual, weight, nullptr, h, y, nullptr, rstd, rows, dim, eps, s);
+    default: return launch_fwd<bf16, false>(x, residual, weight, nullptr, h, y, nullptr, rstd, rows, dim, eps, s);
+  }
+}
+
+extern "C" int scree_add_rmsnorm_bwd(const void* dy, const void* dh, const void* h,
+                                     const void* weight, const float* rstd, void* dx,
+                                     void* dweight, int dparam_dtype, int64_t rows, int64_t dim,
+                                     int dtype, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  const char* fn = "scree_add_rmsnorm_bwd";
+  int rc = validate_common(fn, rows, dim, dtype);
+  if (rc) return rc;
+  if (dweight && !weight) return set_error(SCREE_ERR_INVALID, "%s: dweight requires weight", fn);
+  if (rows == 0 && !dweight) return SCREE_OK;
+  rc = validate_bwd(fn, dy, h, rstd, dx, dweight != nullptr, dparam_dtype, rows, dim, workspace,
+                    workspace_bytes);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case SCREE_DTYPE_F32: return launch_bwd<float, false>(dy, h, weight, nullptr, rstd, dh, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+    case SCREE_DTYPE_F16: return launch_bwd<f16, false>(dy, h, weight, nullptr, rstd, dh, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
+    default: return launch_bwd<bf16, false>(dy, h, weight, nullptr, rstd, dh, dx, dweight, nullptr, dparam_dtype, rows, dim, workspace, s);
   }
 }

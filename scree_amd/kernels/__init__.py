@@ -59,6 +59,28 @@ def varlen_layernorm(arr: Array, weight=None, bias=None, eps: float = 1e-5) -> A
                  ragged_dim=arr.ragged_dim)
 
 
+def varlen_add_rmsnorm(arr: Array, residual, weight=None, eps: float = 1e-6):
+    """Fused ``h = arr + residual`` and ``y = varlen_rmsnorm(h)``; returns ``(h, y)`` as Arrays.
+
+    ``residual`` is an :class:`Array` with the same offsets or a tensor of the
+    values' shape.  Same results, bit for bit, as adding then calling
+    :func:`varlen_rmsnorm` (the reference block's two steps,
+    ``examples/03_train_step.py:46-48``).
+    """
+    import torch
+
+    from .hip import varlen_add_rmsnorm_hip
+
+    _require_device(arr.values, "varlen_add_rmsnorm")
+    if isinstance(residual, Array):
+        if residual.offsets is not arr.offsets and not torch.equal(residual.offsets, arr.offsets):
+            raise ValueError("arr and residual must have identical offsets")
+        residual = residual.values
+    h, y = varlen_add_rmsnorm_hip(arr.values, residual, weight, eps)
+    return (Array(values=h, offsets=arr.offsets, ragged_dim=arr.ragged_dim),
+            Array(values=y, offsets=arr.offsets, ragged_dim=arr.ragged_dim))
+
+
 def varlen_softmax(arr: Array) -> Array:
     """Softmax along the ragged dimension, per sequence (``varlen_softmax.py:13-63``)."""
     from .hip import varlen_softmax_hip
@@ -69,4 +91,5 @@ def varlen_softmax(arr: Array) -> Array:
     return Array(values=varlen_softmax_hip(arr.values, arr.offsets), offsets=arr.offsets, ragged_dim=0)
 
 
-__all__ = ["varlen_attention", "varlen_layernorm", "varlen_rmsnorm", "varlen_softmax"]
+__all__ = ["varlen_add_rmsnorm", "varlen_attention", "varlen_layernorm", "varlen_rmsnorm",
+           "varlen_softmax"]

@@ -15,6 +15,8 @@ from .attention import (
     varlen_attention_hip_backward,
 )
 from .norms import (
+    varlen_add_rmsnorm_hip,
+    varlen_add_rmsnorm_hip_backward,
     varlen_layernorm_hip,
     varlen_layernorm_hip_autograd,
     varlen_layernorm_hip_backward,
@@ -31,6 +33,8 @@ __all__ = [
     "VarlenAttentionHip",
     "attention_schedule",
     "schedule_items",
+    "varlen_add_rmsnorm_hip",
+    "varlen_add_rmsnorm_hip_backward",
     "varlen_attention_hip",
     "varlen_attention_hip_autograd",
     "varlen_attention_hip_backward",

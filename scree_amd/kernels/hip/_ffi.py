@@ -54,6 +54,8 @@ _SIGNATURES = {
     "scree_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),
     "scree_layernorm_fwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _F, _I, _P]),
     "scree_layernorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),
+    "scree_add_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _F, _I, _P]),
+    "scree_add_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _P, _S, _P]),
     "scree_varlen_softmax": (_I, [_P, _P, _P, _I, _L, _L, _I, _P]),
     "scree_varlen_softmax_bwd": (_I, [_P, _P, _P, _P, _I, _L, _L, _I, _P]),
     "scree_to_padded": (_I, [_P, _P, _I, _L, _L, _L, _I, _P, _I, _P, _P, _P]),

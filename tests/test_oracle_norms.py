@@ -120,3 +120,59 @@ def test_properties_unit_rms_and_standardised():
     z, _, _ = layernorm_fwd(x, eps=1e-5)
     np.testing.assert_allclose(z.mean(-1), 0.0, atol=1e-10)
     np.testing.assert_allclose(z.var(-1), 1.0, atol=1e-3)
+
+
+# ------------------------------------------------------ fused add + RMSNorm
+from oracle.norms import add_rmsnorm_bwd, add_rmsnorm_fwd, add_rounded, round_bf16  # noqa: E402
+
+
+def test_round_bf16_matches_torch_conversion():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(20000).astype(np.float32) * np.float32(3.0)
+    # exact ties: bf16 value plus half an ulp, for both parities of the kept bit
+    base = (np.arange(1, 257, dtype=np.uint32) << 16).view(np.float32)
+    ties = (base.view(np.uint32) | 0x8000).view(np.float32)
+    near = np.concatenate([x, ties, np.nextafter(ties, np.float32(np.inf)),
+                           np.nextafter(ties, np.float32(-np.inf)), [0.0, -0.0, 1e-40]]).astype(np.float32)
+    want = torch.from_numpy(near).to(torch.bfloat16).to(torch.float64).numpy()
+    np.testing.assert_array_equal(round_bf16(near), want)
+
+
+@pytest.mark.parametrize("storage,tdtype", [("float16", torch.float16), ("bfloat16", torch.bfloat16),
+                                            ("float32", torch.float32)])
+def test_add_rounded_matches_torch_half_addition(storage, tdtype):
+    rng = np.random.default_rng(6)
+    a = torch.from_numpy(rng.standard_normal(5000)).to(tdtype)
+    b = torch.from_numpy(rng.standard_normal(5000) * 1e-2).to(tdtype)
+    want = (a + b).to(torch.float64).numpy()
+    got = add_rounded(a.to(torch.float64).numpy(), b.to(torch.float64).numpy(), storage)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("with_dh", [False, True])
+def test_add_rmsnorm_matches_torch_autograd(with_dh):
+    rng = np.random.default_rng(7)
+    rows, d = 11, 24
+    x = rng.standard_normal((rows, d))
+    r = rng.standard_normal((rows, d))
+    w = 1 + 0.1 * rng.standard_normal(d)
+    dy = rng.standard_normal((rows, d))
+    dh = rng.standard_normal((rows, d)) if with_dh else None
+    h, y, rstd = add_rmsnorm_fwd(x, r, w, eps=1e-6)
+    xt, rt, wt = (torch.tensor(a, requires_grad=True) for a in (x, r, w))
+    ht = xt + rt
+    yt = F.rms_norm(ht, (d,), wt, eps=1e-6)
+    loss = (yt * torch.tensor(dy)).sum()
+    if with_dh:
+        loss = loss + (ht * torch.tensor(dh)).sum()
+    loss.backward()
+    np.testing.assert_allclose(h, ht.detach().numpy(), atol=1e-14)
+    np.testing.assert_allclose(y, yt.detach().numpy(), atol=1e-12)
+    dx, dw = add_rmsnorm_bwd(dy, dh, h, w, eps=1e-6)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), atol=1e-11)
+    np.testing.assert_allclose(dx, rt.grad.numpy(), atol=1e-11)
+    np.testing.assert_allclose(dw, wt.grad.numpy(), atol=1e-11)
+    # the fused forward is the unfused composition
+    y2, rstd2 = rmsnorm_fwd(add_rounded(x, r), w, eps=1e-6)
+    np.testing.assert_array_equal(y, y2)
+    np.testing.assert_array_equal(rstd, rstd2)
