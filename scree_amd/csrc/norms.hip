@@ -187,6 +187,131 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_generic(
 constexpr int kBwdThreads = 512;
 constexpr int kBwdWarps = kBwdThreads / kWave;
 
+// One step's rows: this thread's 16-byte vectors of x, dy (and dres) for R
+// rows, with the rows' statistics.  The kernel keeps two of these and loads
+// the next step's rows while it reduces and writes the current one.
+template <typename T, int CPT, int R, bool LAYER, bool RES>
+struct BwdRows {
+  uint4 xv[R][CPT], gv[R][CPT], hv[RES ? R : 1][CPT];
+  float rs[R], mu[R];
+
+  __device__ __forceinline__ void load(const T* __restrict__ x, const T* __restrict__ dy,
+                                       const T* __restrict__ dres,
+                                       const float* __restrict__ mean_in,
+                                       const float* __restrict__ rstd_in, const bool* own,
+                                       int64_t rb, int64_t r1, int dim, int tid) {
+    constexpr int VEC = 16 / sizeof(T);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = rb + r;
+      const bool ok = row < r1;
+      rs[r] = ok ? rstd_in[row] : 0.f;
+      mu[r] = (LAYER && ok) ? mean_in[row] : 0.f;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int64_t off = row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC;
+        xv[r][k] = (ok && own[k]) ? ld16_nt(x + off) : make_uint4(0, 0, 0, 0);
+        gv[r][k] = (ok && own[k]) ? ld16_nt(dy + off) : make_uint4(0, 0, 0, 0);
+        if (RES) hv[r][k] = (ok && own[k]) ? ld16_nt(dres + off) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+};
+
+// The rows of one step: row sums reduced across the wave by shuffles and
+// across the block through red[buf] (one barrier), then dx written and the
+// parameter gradients accumulated in aw / ab.
+template <typename T, int CPT, int R, bool LAYER, bool RES>
+__device__ __forceinline__ void norm_bwd_step(BwdRows<T, CPT, R, LAYER, RES>& st,
+                                              float (&red)[2][R][2][kBwdWarps], int buf,
+                                              const uint4* wv, const bool* own, bool has_w,
+                                              float (&aw)[CPT][16 / sizeof(T)],
+                                              float (&ab)[LAYER ? CPT : 1][16 / sizeof(T)],
+                                              T* __restrict__ dx, int64_t rb, int64_t r1, int dim,
+                                              int tid) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const float fdim = (float)dim;
+  float s1[R], s2[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    s1[r] = 0.f;
+    s2[r] = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xx = elem<T>(st.xv[r][k], e);
+        const float d = elem<T>(st.gv[r][k], e);
+        const float g = has_w ? d * elem<T>(wv[k], e) : d;
+        if (LAYER) {
+          s1[r] += g;
+          s2[r] += g * ((xx - st.mu[r]) * st.rs[r]);
+        } else {
+          s1[r] += xx * g;
+        }
+      }
+    s1[r] = wave_sum(s1[r]);
+    if (LAYER) s2[r] = wave_sum(s2[r]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      red[buf][r][0][wave] = s1[r];
+      red[buf][r][1][wave] = s2[r];
+    }
+  }
+  __syncthreads();
+  // Keep the rows packed across the barrier: re-derive the fp32 values
+  // below instead of holding the converted floats live.
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      asm volatile("" : "+v"(st.xv[r][k].x), "+v"(st.xv[r][k].y), "+v"(st.xv[r][k].z), "+v"(st.xv[r][k].w));
+      asm volatile("" : "+v"(st.gv[r][k].x), "+v"(st.gv[r][k].y), "+v"(st.gv[r][k].z), "+v"(st.gv[r][k].w));
+      if (RES)
+        asm volatile("" : "+v"(st.hv[RES ? r : 0][k].x), "+v"(st.hv[RES ? r : 0][k].y),
+                     "+v"(st.hv[RES ? r : 0][k].z), "+v"(st.hv[RES ? r : 0][k].w));
+    }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < kBwdWarps; ++q) {
+      t1 += red[buf][r][0][q];
+      if (LAYER) t2 += red[buf][r][1][q];
+    }
+    const int64_t row = rb + r;
+    if (row >= r1) continue;
+    const float rr = st.rs[r];
+    const float k_rms = rr * rr * rr * t1 / fdim;
+    const float a_ln = t1 / fdim, b_ln = t2 / fdim;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      if (!own[k]) continue;
+      float f[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xx = elem<T>(st.xv[r][k], e);
+        const float d = elem<T>(st.gv[r][k], e);
+        const float g = has_w ? d * elem<T>(wv[k], e) : d;
+        if (LAYER) {
+          const float xh = (xx - st.mu[r]) * rr;
+          f[e] = rr * (g - a_ln - xh * b_ln);
+          aw[k][e] += d * xh;
+          ab[LAYER ? k : 0][e] += d;
+        } else {
+          f[e] = rr * g - k_rms * xx;
+          aw[k][e] += d * xx * rr;
+        }
+        if (RES) f[e] += elem<T>(st.hv[RES ? r : 0][k], e);
+      }
+      st16_nt(dx + row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC, pack16<T>(f));
+    }
+  }
+}
+
 // RES: dx also receives dres (the gradient reaching the normalised input by
 // another path, e.g. the residual stream of an add + RMSNorm).
 template <typename T, int CPT, int R, bool LAYER, bool RES>
@@ -197,9 +322,8 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
     int dim, int nparam, int64_t rows_per_block) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float red[2][R][2][kBwdWarps];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int tid = threadIdx.x;
   const int nvec = dim / VEC;
-  const float fdim = (float)dim;
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
   const int64_t r1 = min(rows, r0 + rows_per_block);
 
@@ -220,102 +344,16 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
       ab[LAYER ? k : 0][e] = 0.f;
     }
 
-  int buf = 0;
-  for (int64_t rb = r0; rb < r1; rb += R) {
-    uint4 xv[R][CPT], gv[R][CPT], hv[RES ? R : 1][CPT];
-    float rs[R], mu[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t row = rb + r;
-      const bool ok = row < r1;
-      rs[r] = ok ? rstd_in[row] : 0.f;
-      mu[r] = (LAYER && ok) ? mean_in[row] : 0.f;
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        const int64_t off = row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC;
-        xv[r][k] = (ok && own[k]) ? ld16_nt(x + off) : make_uint4(0, 0, 0, 0);
-        gv[r][k] = (ok && own[k]) ? ld16_nt(dy + off) : make_uint4(0, 0, 0, 0);
-        if (RES) hv[r][k] = (ok && own[k]) ? ld16_nt(dres + off) : make_uint4(0, 0, 0, 0);
-      }
-    }
-    float s1[R], s2[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      s1[r] = 0.f;
-      s2[r] = 0.f;
-#pragma unroll
-      for (int k = 0; k < CPT; ++k)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float xx = elem<T>(xv[r][k], e);
-          const float d = elem<T>(gv[r][k], e);
-          const float g = w ? d * elem<T>(wv[k], e) : d;
-          if (LAYER) {
-            s1[r] += g;
-            s2[r] += g * ((xx - mu[r]) * rs[r]);
-          } else {
-            s1[r] += xx * g;
-          }
-        }
-      s1[r] = wave_sum(s1[r]);
-      if (LAYER) s2[r] = wave_sum(s2[r]);
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        red[buf][r][0][wave] = s1[r];
-        red[buf][r][1][wave] = s2[r];
-      }
-    }
-    __syncthreads();
-    // Keep x and dy packed across the barrier: re-derive the fp32 values
-    // below instead of holding 2*R*CPT*VEC converted floats live.
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        asm volatile("" : "+v"(xv[r][k].x), "+v"(xv[r][k].y), "+v"(xv[r][k].z), "+v"(xv[r][k].w));
-        asm volatile("" : "+v"(gv[r][k].x), "+v"(gv[r][k].y), "+v"(gv[r][k].z), "+v"(gv[r][k].w));
-        if (RES)
-          asm volatile("" : "+v"(hv[RES ? r : 0][k].x), "+v"(hv[RES ? r : 0][k].y),
-                       "+v"(hv[RES ? r : 0][k].z), "+v"(hv[RES ? r : 0][k].w));
-      }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float t1 = 0.f, t2 = 0.f;
-#pragma unroll
-      for (int q = 0; q < kBwdWarps; ++q) {
-        t1 += red[buf][r][0][q];
-        if (LAYER) t2 += red[buf][r][1][q];
-      }
-      const int64_t row = rb + r;
-      if (row >= r1) continue;
-      const float k_rms = rs[r] * rs[r] * rs[r] * t1 / fdim;
-      const float a_ln = t1 / fdim, b_ln = t2 / fdim;
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        if (!own[k]) continue;
-        float f[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float xx = elem<T>(xv[r][k], e);
-          const float d = elem<T>(gv[r][k], e);
-          const float g = w ? d * elem<T>(wv[k], e) : d;
-          if (LAYER) {
-            const float xh = (xx - mu[r]) * rs[r];
-            f[e] = rs[r] * (g - a_ln - xh * b_ln);
-            aw[k][e] += d * xh;
-            ab[LAYER ? k : 0][e] += d;
-          } else {
-            f[e] = rs[r] * g - k_rms * xx;
-            aw[k][e] += d * xx * rs[r];
-          }
-          if (RES) f[e] += elem<T>(hv[RES ? r : 0][k], e);
-        }
-        st16_nt(dx + row * (int64_t)dim + (int64_t)(tid + k * kBwdThreads) * VEC, pack16<T>(f));
-      }
-    }
-    buf ^= 1;
+  // Two row sets: while one step reduces and writes, the next step's rows load.
+  BwdRows<T, CPT, R, LAYER, RES> A, B;
+  const bool has_w = w != nullptr;
+  if (r0 < r1) A.load(x, dy, dres, mean_in, rstd_in, own, r0, r1, dim, tid);
+  for (int64_t rb = r0; rb < r1; rb += 2 * R) {
+    if (rb + R < r1) B.load(x, dy, dres, mean_in, rstd_in, own, rb + R, r1, dim, tid);
+    norm_bwd_step<T, CPT, R, LAYER, RES>(A, red, 0, wv, own, has_w, aw, ab, dx, rb, r1, dim, tid);
+    if (rb + R >= r1) break;
+    if (rb + 2 * R < r1) A.load(x, dy, dres, mean_in, rstd_in, own, rb + 2 * R, r1, dim, tid);
+    norm_bwd_step<T, CPT, R, LAYER, RES>(B, red, 1, wv, own, has_w, aw, ab, dx, rb + R, r1, dim, tid);
   }
   for (int p = 0; p < nparam; ++p) {
     float* out = partial + ((int64_t)blockIdx.x * nparam + p) * dim;
@@ -575,10 +613,10 @@ void launch_bwd_k(const T* dyp, const T* xp, const T* wp, const float* mean, con
     const int64_t rpb = rows_per_part(rows, nparts);
     const dim3 grid((unsigned)nparts), block(kBwdThreads);
     const int np = want_params ? nparam : 0;
-    // rows per step: as many as fit 4 waves per SIMD (LN keeps two sums per
-    // row; the residual gradient is one more vector per row)
-    constexpr int R1 = (LAYER || RES) ? 4 : 8;
-    constexpr int R2 = (LAYER || RES) ? 2 : 4;
+    // rows per step: two steps' rows (double-buffered) fit 4 waves per SIMD
+    // (LN keeps two sums per row; the residual gradient is one more vector)
+    constexpr int R1 = (LAYER || RES) ? 2 : 4;
+    constexpr int R2 = (LAYER || RES) ? 1 : 2;
     if (cpt == 1)
       hipLaunchKernelGGL((norm_bwd_cols<T, 1, R1, LAYER, RES>), grid, block, 0, stream, dyp, xp, wp,
                          mean, rstd, dresp, dxp, partial, rows, d, np, rpb);
