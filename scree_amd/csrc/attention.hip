@@ -282,6 +282,19 @@ __device__ __forceinline__ void mask_rows_above(f32x16& c, int rel_minus_4g) {
 // Wave index as a scalar, so per-wave tile bounds are uniform branches.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
 
+// Workgroup barrier once this wave's LDS accesses have completed and at most
+// its newest N vector-memory operations are still in flight.  Written without
+// a fence: __syncthreads()'s release fence waits for every outstanding LDS
+// write, direct-to-LDS DMA included, which would drain a DMA issued for a
+// later block.  The memory clobber keeps the compiler from moving memory
+// accesses across it; DMA data in LDS is visible to the workgroup once the
+// issuing wave's vmcnt has counted it.
+template <int N>
+__device__ __forceinline__ void barrier_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 struct Strides {
   int64_t row, head;
 };
@@ -428,11 +441,6 @@ __device__ __forceinline__ void half_pair(float x, float& a, float& b) {
   a = lo;
   b = hi;
 }
-__device__ __forceinline__ float halves_max(float x) {
-  float a, b;
-  half_pair(x, a, b);
-  return fmaxf(a, b);
-}
 __device__ __forceinline__ float halves_sum(float x) {
   float a, b;
   half_pair(x, a, b);
@@ -453,6 +461,7 @@ struct FwdState {
   int2 voffs[D / 32];       // swizzled V transposed-read offsets
   f32x16 oacc[D / 32];      // O^T accumulators
   float m_run, l_run;       // running max (raw scores) and row sum (this lane's keys)
+  float m_thresh, neg_mb;   // m_run + rescale_gap and -m_run * scale_log2 (change on rescale)
   DmaTile<T, D, kBN> dK, dV;
   const T* kh;
   const T* vh;
@@ -460,6 +469,15 @@ struct FwdState {
   int L, nkb, kend_wave, qw0, wave, lr, g;
   float scale_log2, rescale_gap;
 };
+
+// v_max3_f32 written out: for fmaxf the compiler first canonicalises every
+// operand it cannot prove is not a signalling NaN (each MFMA result), one
+// extra instruction each.  Scores are MFMA results or -inf, never signalling.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 // One 64-key block kb: start the DMA of block kb + 1 into `nxt`, then compute
 // on `cur` (K tile, then V tile).  The restrict qualifiers tell the compiler
@@ -499,11 +517,18 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
     } else if (tbase + 32 > st.L) {
       mask_rows_above(sacc, st.L - 1 - tbase - 4 * st.g);
     }
-    float mx = sacc[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
-    mx = halves_max(mx);
-    const bool grow = mx > st.m_run + st.rescale_gap;
+    // tile max: two interleaved max3 chains, then across the wave's halves
+    float ma = max3f(sacc[0], sacc[1], sacc[2]);
+    float mc = max3f(sacc[3], sacc[4], sacc[5]);
+    ma = max3f(ma, sacc[6], sacc[7]);
+    mc = max3f(mc, sacc[8], sacc[9]);
+    ma = max3f(ma, sacc[10], sacc[11]);
+    mc = max3f(mc, sacc[12], sacc[13]);
+    ma = max3f(ma, sacc[14], sacc[15]);
+    float lo, hi;
+    half_pair(max3f(ma, mc, mc), lo, hi);
+    const float mx = max3f(lo, hi, hi);
+    const bool grow = mx > st.m_thresh;
     if (__any(grow)) {
       const float m_new = grow ? mx : st.m_run;
       const float alpha = fast_exp2((st.m_run - m_new) * st.scale_log2);
@@ -513,15 +538,19 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
 #pragma unroll
         for (int i = 0; i < 16; ++i) st.oacc[dt][i] *= alpha;
       st.m_run = m_new;
+      st.m_thresh = m_new + st.rescale_gap;
+      st.neg_mb = -m_new * st.scale_log2;
     }
-    const float mb = st.m_run * st.scale_log2;
-    float ls[2] = {st.l_run, 0.f};  // the row sum in fp32, of the unrounded weights
+    // the row sum in fp32, of the unrounded weights (two partial chains)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      sacc[i] = fast_exp2(fmaf(sacc[i], st.scale_log2, -mb));
-      ls[i & 1] += sacc[i];
+    for (int i = 0; i < 16; ++i) sacc[i] = fast_exp2(fmaf(sacc[i], st.scale_log2, st.neg_mb));
+    float ls0 = st.l_run + sacc[0], ls1 = sacc[1];
+#pragma unroll
+    for (int i = 2; i < 16; i += 2) {
+      ls0 += sacc[i];
+      ls1 += sacc[i + 1];
     }
-    st.l_run = ls[0] + ls[1];
+    st.l_run = ls0 + ls1;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const x8 pf = pack_frag<T>(sacc, 8 * hh);
@@ -594,6 +623,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   for (int dt = 0; dt < D / 32; ++dt) st.oacc[dt] = zero16();
   st.m_run = kMaxInit;
   st.l_run = 0.f;
+  st.m_thresh = kMaxInit + st.rescale_gap;
+  st.neg_mb = -kMaxInit * scale_log2;
 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -639,17 +670,27 @@ struct DqState {
   float scale_log2;
 };
 
-// One 64-key block kb (see fwd_block for the buffer discipline).
-template <typename T, int D, bool CAUSAL>
+// Number of K/V tile buffers of the dQ pass: three (the DMA runs two blocks
+// ahead) where the third costs no occupancy, two at D = 128.
+template <int D>
+constexpr int dq_nbuf() {
+  return D <= 64 ? 3 : 2;
+}
+
+// One 64-key block kb on `cur` while the DMA of block kb + AHEAD fills `nxt`
+// (see fwd_block for the buffer discipline).  Ends with a barrier once block
+// kb + 1 has landed; block kb + 2's DMA may stay in flight across it.
+template <typename T, int D, bool CAUSAL, int AHEAD>
 __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __restrict__ cur,
                                          T* __restrict__ nxt) {
   typedef typename VecT<T>::x8 x8;
   constexpr int TILE = kBN * D;
+  constexpr int NL = 2 * DmaTile<T, D, kBN>::PER_WAVE;  // DMA instructions per block
   const T* sK = cur;
   const T* sV = cur + TILE;
-  if (kb + 1 < st.nkb) {
-    st.dK.load(nxt, st.kh, st.krow, (kb + 1) * kBN, st.L, st.wave);
-    st.dV.load(nxt + TILE, st.vh, st.vrow, (kb + 1) * kBN, st.L, st.wave);
+  if (kb + AHEAD < st.nkb) {
+    st.dK.load(nxt, st.kh, st.krow, (kb + AHEAD) * kBN, st.L, st.wave);
+    st.dV.load(nxt + TILE, st.vh, st.vrow, (kb + AHEAD) * kBN, st.L, st.wave);
   }
   const int kbase = kb * kBN;
   const int nt = kbase < st.kend_wave ? (kbase + 32 < st.kend_wave ? 2 : 1) : 0;
@@ -677,8 +718,53 @@ __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __r
                               st.dqacc[dt]);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block kb + 1 has landed
-  __syncthreads();
+  // No other vector-memory operations run in the loop, so at most NL are
+  // younger than this wave's share of block kb + 1: block kb + 2's.
+  if (AHEAD == 2 && kb + 2 < st.nkb)
+    barrier_vm<NL>();
+  else
+    barrier_vm<0>();
+}
+
+// The dQ block loop over tile buffers A, B (and C): stages blocks 0 (and 1),
+// runs `setup` while they fly, then loops.  Every DMA and tile read sits in
+// this one function, so the compiler's alias scopes tell each pending DMA
+// apart from the reads of the other buffers (a DMA pending across two calls
+// of dq_block would otherwise make it wait for the DMA before every read).
+template <typename T, int D, bool CAUSAL, typename Setup>
+__device__ __forceinline__ void dq_run(DqState<T, D>& st, T* __restrict__ A, T* __restrict__ B,
+                                       T* __restrict__ C, Setup setup) {
+  constexpr int TILE = kBN * D;
+  constexpr int NL = 2 * DmaTile<T, D, kBN>::PER_WAVE;
+  constexpr bool three = dq_nbuf<D>() == 3;
+  st.dK.load(A, st.kh, st.krow, 0, st.L, st.wave);
+  st.dV.load(A + TILE, st.vh, st.vrow, 0, st.L, st.wave);
+  if (three && st.nkb > 1) {
+    st.dK.load(B, st.kh, st.krow, kBN, st.L, st.wave);
+    st.dV.load(B + TILE, st.vh, st.vrow, kBN, st.L, st.wave);
+  }
+  setup();
+  // The count is safe with setup's own loads and stores in flight: they can
+  // only add to it, and loads retire in order.
+  if (three && st.nkb > 1)
+    barrier_vm<NL>();
+  else
+    barrier_vm<0>();
+  if constexpr (three) {
+    for (int kb = 0; kb < st.nkb; kb += 3) {
+      dq_block<T, D, CAUSAL, 2>(st, kb, A, C);
+      if (kb + 1 >= st.nkb) break;
+      dq_block<T, D, CAUSAL, 2>(st, kb + 1, B, A);
+      if (kb + 2 >= st.nkb) break;
+      dq_block<T, D, CAUSAL, 2>(st, kb + 2, C, B);
+    }
+  } else {
+    for (int kb = 0; kb < st.nkb; kb += 2) {
+      dq_block<T, D, CAUSAL, 1>(st, kb, A, B);
+      if (kb + 1 >= st.nkb) break;
+      dq_block<T, D, CAUSAL, 1>(st, kb + 1, B, A);
+    }
+  }
 }
 
 template <typename T, int D, bool CAUSAL>
@@ -691,7 +777,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   typedef typename VecT<T>::x8 x8;
   constexpr int TILE = kBN * D;
   constexpr int BUF = 2 * TILE;  // K tile then V tile
-  __shared__ __align__(16) T smem[2 * BUF];
+  __shared__ __align__(16) T smem[dq_nbuf<D>() * BUF];
 
   int item, h;
   if (!map_block(heads, tmax, head_major, group, item, h) || item >= header[0]) return;
@@ -715,51 +801,44 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   st.nkb = (kend_wg + kBN - 1) / kBN;
   st.kend_wave = wave_live ? (CAUSAL ? min(L, st.qw0 + 32) : L) : 0;
 
-  T* bufA = smem;
-  T* bufB = smem + BUF;
   st.dK.init(sk.row, st.wave, lane);
   st.dV.init(sv.row, st.wave, lane);
-  st.dK.load(bufA, st.kh, sk.row, 0, L, st.wave);
-  st.dV.load(bufA + TILE, st.vh, sv.row, 0, L, st.wave);
 
-  float dl = 0.f;
-  {  // rows past L read row L-1: their results are never stored
-    const int64_t tok = start + min(my_q, L - 1);
-    const T* qrow = q + tok * sq.row + (int64_t)h * sq.head;
-    const T* drow = dout + tok * sdo.row + (int64_t)h * sdo.head;
-    const T* orow = o + tok * so.row + (int64_t)h * so.head;
+  // This wave's query rows, Delta and fragment offsets, set up while the
+  // first K/V blocks are in flight.
+  auto setup = [&] {
+    float dl = 0.f;
+    {  // rows past L read row L-1: their results are never stored
+      const int64_t tok = start + min(my_q, L - 1);
+      const T* qrow = q + tok * sq.row + (int64_t)h * sq.head;
+      const T* drow = dout + tok * sdo.row + (int64_t)h * sdo.head;
+      const T* orow = o + tok * so.row + (int64_t)h * so.head;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
-      st.df[s] = gmem_frag16(drow + 16 * s + 8 * st.g);
-      const x8 of = gmem_frag16(orow + 16 * s + 8 * st.g);
+      for (int s = 0; s < D / 16; ++s) {
+        st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
+        st.df[s] = gmem_frag16(drow + 16 * s + 8 * st.g);
+        const x8 of = gmem_frag16(orow + 16 * s + 8 * st.g);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)st.df[s][j];
+        for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)st.df[s][j];
+      }
+      st.lse2 = lse[tok * heads + h] * kLog2e;
+      // Materialize the fragments before the barrier (see the forward).
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.qf[s]), "+v"(st.df[s]));
     }
-    st.lse2 = lse[tok * heads + h] * kLog2e;
-    // Materialize the fragments before the barrier (see the forward).
+    dl = halves_sum(dl);
+    if (my_q < L && st.g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.qf[s]), "+v"(st.df[s]));
-  }
-  dl = halves_sum(dl);
-  if (my_q < L && st.g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
+    for (int i = 0; i < 16; ++i) st.neg_delta[i] = -dl;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) st.neg_delta[i] = -dl;
+    for (int s = 0; s < D / 16; ++s) st.koff[s] = swz_off<D>(st.lr, 2 * s + st.g);
 #pragma unroll
-  for (int s = 0; s < D / 16; ++s) st.koff[s] = swz_off<D>(st.lr, 2 * s + st.g);
+    for (int dt = 0; dt < D / 32; ++dt) st.ktr[dt] = swz_tr_off<D>(st.lr, st.g, dt);
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) st.ktr[dt] = swz_tr_off<D>(st.lr, st.g, dt);
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) st.dqacc[dt] = zero16();
-  st.scale_log2 = scale_log2;
-
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  // Unrolled by two so that each call sees its buffers at fixed positions.
-  for (int kb = 0; kb < st.nkb; kb += 2) {
-    dq_block<T, D, CAUSAL>(st, kb, bufA, bufB);
-    if (kb + 1 < st.nkb) dq_block<T, D, CAUSAL>(st, kb + 1, bufB, bufA);
-  }
+    for (int dt = 0; dt < D / 32; ++dt) st.dqacc[dt] = zero16();
+    st.scale_log2 = scale_log2;
+  };
+  dq_run<T, D, CAUSAL>(st, smem, smem + BUF, dq_nbuf<D>() == 3 ? smem + 2 * BUF : nullptr, setup);
   if (wave_live && my_q < L) {
     T* out = dq + (int64_t)(start + my_q) * sdq.row + (int64_t)h * sdq.head;
 #pragma unroll
