@@ -7,21 +7,33 @@
 // / numpy per slice); it has no GPU kernel.
 //
 // Layout: x, y contiguous (total_tokens, features).  One workgroup per
-// (sequence, column chunk): its 256 threads are `ct` column lanes (each owning
-// VEC adjacent columns, one 16-byte vector when the row allows it) times
-// `256 / ct` row lanes that stride over the sequence's rows.  Pass 1 keeps an
+// (sequence, column chunk): its 256 threads (512 in the backward) are `ct`
+// column lanes (each owning VEC adjacent columns, one 16-byte vector when the
+// row allows it) times `threads / ct` row lanes that stride over the
+// sequence's rows.  Pass 1 keeps an
 // online (max, sum) per column with one exp per element; the row lanes merge
-// through LDS; pass 2 re-reads the rows (the tensor is usually still in the
-// L2 / MALL) and writes the normalised values with streaming stores.
+// through LDS; pass 2 writes the normalised values with streaming stores.
+// When the sequence has at most kSmCache rows per row lane (checked per
+// workgroup), every thread keeps its rows as loaded in registers: pass 1
+// takes the thread's max and then its sum of exponentials, and pass 2 reads
+// the rows from there, so x is read once.  Longer sequences use the online
+// update and re-read their rows in pass 2 (the tensor is then usually still
+// in the L2 / MALL).  Row lanes merge by a fixed tree: results are
+// deterministic.
 // Statistics are fp32 for every input dtype; y has x's dtype.
+
+#include <type_traits>
 
 #include "common.h"
 
 namespace scree {
 namespace {
 
-constexpr int kSmThreads = 256;
-constexpr int kUnroll = 4;          // rows per thread per loop trip (loads issued together)
+constexpr int kSmThreads = 256;        // forward: more, smaller workgroups overlap their phases
+constexpr int kSmThreadsBwd = 512;     // backward: more row lanes, so that held rows cover longer sequences
+constexpr int kUnroll = 4;              // rows per thread per loop trip (loads issued together)
+constexpr int kSmCache = 16;            // forward: rows per thread held in registers between the passes
+constexpr int kSmCacheBwd = 10;         // backward (y and dy held): 2 workgroups per CU
 constexpr int64_t kSmMinBlocks = 2048;  // narrow the column lanes until the grid is this big
 constexpr float kLog2eSm = 1.4426950408889634f;
 
@@ -47,6 +59,54 @@ struct Vec {
   }
 };
 
+// One row's VEC columns kept in registers as loaded (16 bytes, or one value).
+template <typename T, int VEC>
+struct Held {
+  typename std::conditional<VEC == 1, float, uint4>::type v;
+  __device__ __forceinline__ void load(const T* p) {
+    if constexpr (VEC == 1)
+      v = to_f32(*p);
+    else
+      v = ld16(p);
+  }
+  __device__ __forceinline__ void get(float* f) const {
+    if constexpr (VEC == 1) {
+      f[0] = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) f[e] = elem<T>(v, e);
+    }
+  }
+};
+
+// Online (max, sum) update with one exp per element: scale whichever of
+// (sum, new term) is behind.
+__device__ __forceinline__ void sm_update(float& m, float& l, float v) {
+  const float hi = fmaxf(m, v);
+  const float t = hi == -__builtin_inff()
+                      ? 0.f  // -inf so far: nothing to add (avoids -inf - -inf)
+                      : __builtin_amdgcn_exp2f((fminf(m, v) - hi) * kLog2eSm);
+  l = v > m ? fmaf(l, t, 1.0f) : l + t;
+  m = hi;
+}
+
+// v_max3_f32 written out (fmaxf adds a canonicalising instruction per
+// operand it cannot prove quiet, i.e. every loaded value).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Merge the partial (max, sum) of another row lane into (m, l).
+__device__ __forceinline__ void sm_merge(float& m, float& l, float m2, float l2) {
+  const float hi = fmaxf(m, m2);
+  const float a = m == -__builtin_inff() ? 0.f : l * __builtin_amdgcn_exp2f((m - hi) * kLog2eSm);
+  const float b = m2 == -__builtin_inff() ? 0.f : l2 * __builtin_amdgcn_exp2f((m2 - hi) * kLog2eSm);
+  l = a + b;
+  m = hi;
+}
+
 template <typename T, int VEC>
 __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
     const T* __restrict__ x, T* __restrict__ y, const int32_t* __restrict__ cu, int64_t total,
@@ -61,6 +121,7 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
   const int tc = threadIdx.x % ct, tr = threadIdx.x / ct;
   const int64_t col = ((int64_t)chunk * ct + tc) * VEC;
   const bool active = col < features;  // VEC > 1 only when features % VEC == 0
+  const bool cached = end - start <= (int64_t)kSmCache * rs;  // uniform per workgroup
 
   float m[VEC], l[VEC];
 #pragma unroll
@@ -68,53 +129,74 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
     m[e] = -__builtin_inff();
     l[e] = 0.f;
   }
+  Held<T, VEC> held[kSmCache];
   if (active) {
-    for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
-      float v[kUnroll][VEC];  // kUnroll rows' loads in flight before any math
+    if (cached) {
+      // every load in flight before any math; rows past the end stay unread
+      const int nr = (int)min<int64_t>(kSmCache, (end - start - tr + rs - 1) / rs);  // rows held
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (r + u * rs < end) {
-          Vec<T, VEC>::load(x + (r + u * rs) * features + col, v[u]);
-        } else {
+      for (int i = 0; i < kSmCache; ++i)
+        if (i < nr) held[i].load(x + (start + tr + (int64_t)i * rs) * features + col);
+      // With the rows at hand, the thread's max first and then the sum of
+      // exponentials against it (fewer instructions than the online update).
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) v[u][e] = -__builtin_inff();
-        }
+      for (int i = 0; i < kSmCache; i += 2) {
+        if (i >= nr) continue;
+        float a[VEC], b[VEC];
+        held[i].get(a);
+        if (i + 1 < nr)
+          held[i + 1].get(b);
+        else
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) b[e] = a[e];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) m[e] = max3f(m[e], a[e], b[e]);
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
+      for (int i = 0; i < kSmCache; ++i) {
+        if (i >= nr) continue;
+        float v[VEC];
+        held[i].get(v);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          // one exp per element: scale whichever of (sum, new term) is behind
-          const float hi = fmaxf(m[e], v[u][e]);
-          const float t = hi == -__builtin_inff()
-                              ? 0.f  // -inf so far: nothing to add (avoids -inf - -inf)
-                              : __builtin_amdgcn_exp2f((fminf(m[e], v[u][e]) - hi) * kLog2eSm);
-          l[e] = v[u][e] > m[e] ? fmaf(l[e], t, 1.0f) : l[e] + t;
-          m[e] = hi;
+        for (int e = 0; e < VEC; ++e)  // m = -inf: every value is -inf, nothing to add
+          l[e] += m[e] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f((v[e] - m[e]) * kLog2eSm);
+      }
+    } else {
+      for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
+        float v[kUnroll][VEC];  // kUnroll rows' loads in flight before any math
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          if (r + u * rs < end) {
+            Vec<T, VEC>::load(x + (r + u * rs) * features + col, v[u]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) v[u][e] = -__builtin_inff();  // a no-op update
+          }
         }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) sm_update(m[e], l[e], v[u][e]);
+      }
     }
   }
-  // merge the row lanes of each column (fixed order: deterministic)
+  // merge the row lanes of each column: a tree over the (power-of-two) row
+  // lanes in LDS, log2(rs) steps in a fixed order (deterministic)
 #pragma unroll
   for (int e = 0; e < VEC; ++e) {
     s_m[threadIdx.x * VEC + e] = m[e];
     s_l[threadIdx.x * VEC + e] = l[e];
   }
-  __syncthreads();
-  if (tr == 0) {
+  for (int h = rs >> 1; h >= 1; h >>= 1) {
+    __syncthreads();
+    if (tr < h) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      float mm = m[e];
-      for (int j = 1; j < rs; ++j) mm = fmaxf(mm, s_m[(j * ct + tc) * VEC + e]);
-      float ll = 0.f;
-      for (int j = 0; j < rs; ++j) {
-        const float mj = s_m[(j * ct + tc) * VEC + e];
-        ll += mj == -__builtin_inff() ? 0.f
-                                      : s_l[(j * ct + tc) * VEC + e] *
-                                            __builtin_amdgcn_exp2f((mj - mm) * kLog2eSm);
+      for (int e = 0; e < VEC; ++e) {
+        const int o = ((tr + h) * ct + tc) * VEC + e;
+        sm_merge(m[e], l[e], s_m[o], s_l[o]);
+        s_m[threadIdx.x * VEC + e] = m[e];
+        s_l[threadIdx.x * VEC + e] = l[e];
       }
-      m[e] = mm;
-      l[e] = ll;
     }
   }
   __syncthreads();
@@ -133,6 +215,19 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
     mm[e] = s_m[tc * VEC + e];
     inv[e] = s_l[tc * VEC + e];
   }
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kSmCache; ++i) {
+      const int64_t r = start + tr + (int64_t)i * rs;
+      if (r >= end) continue;  // (not break: a fixed trip count keeps the array in registers)
+      float v[VEC];
+      held[i].get(v);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = __builtin_amdgcn_exp2f((v[e] - mm[e]) * kLog2eSm) * inv[e];
+      Vec<T, VEC>::store(y + r * features + col, v);
+    }
+    return;
+  }
   for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
     float v[kUnroll][VEC];
 #pragma unroll
@@ -150,51 +245,77 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
 }
 
 // Backward: dx = y * (dy - s) with s = sum over the sequence's rows of y * dy,
-// per column; same decomposition as the forward.
+// per column; same decomposition as the forward (y and dy held in registers
+// when the sequence fits).
 template <typename T, int VEC>
-__global__ __launch_bounds__(kSmThreads) void varlen_softmax_bwd_kernel(
+__global__ __launch_bounds__(kSmThreadsBwd) void varlen_softmax_bwd_kernel(
     const T* __restrict__ y, const T* __restrict__ dy, T* __restrict__ dx,
     const int32_t* __restrict__ cu, int64_t total, int64_t features, int ct, int chunks) {
-  __shared__ float s_s[kSmThreads * VEC];
+  __shared__ float s_s[kSmThreadsBwd * VEC];
   const int seq = blockIdx.x / chunks, chunk = blockIdx.x - seq * chunks;
   const int64_t start = min<int64_t>(max<int64_t>(cu[seq], 0), total);
   const int64_t end = min<int64_t>(max<int64_t>(cu[seq + 1], start), total);
-  const int rs = kSmThreads / ct;
+  const int rs = kSmThreadsBwd / ct;
   const int tc = threadIdx.x % ct, tr = threadIdx.x / ct;
   const int64_t col = ((int64_t)chunk * ct + tc) * VEC;
   const bool active = col < features;
+  const bool cached = end - start <= (int64_t)kSmCacheBwd * rs;  // uniform per workgroup
 
   float acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  Held<T, VEC> hy[kSmCacheBwd], hd[kSmCacheBwd];
   if (active) {
-    for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
-      float a[kUnroll][VEC], b[kUnroll][VEC];
+    if (cached) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (r + u * rs < end) {
-          Vec<T, VEC>::load(y + (r + u * rs) * features + col, a[u]);
-          Vec<T, VEC>::load(dy + (r + u * rs) * features + col, b[u]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) a[u][e] = b[u][e] = 0.f;
+      for (int i = 0; i < kSmCacheBwd; ++i) {
+        const int64_t r = start + tr + (int64_t)i * rs;
+        if (r < end) {
+          hy[i].load(y + r * features + col);
+          hd[i].load(dy + r * features + col);
         }
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
+      for (int i = 0; i < kSmCacheBwd; ++i) {
+        const int64_t r = start + tr + (int64_t)i * rs;
+        if (r >= end) continue;
+        float a[VEC], b[VEC];
+        hy[i].get(a);
+        hd[i].get(b);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(a[u][e], b[u][e], acc[e]);
+        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(a[e], b[e], acc[e]);
+      }
+    } else {
+      for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
+        float a[kUnroll][VEC], b[kUnroll][VEC];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          if (r + u * rs < end) {
+            Vec<T, VEC>::load(y + (r + u * rs) * features + col, a[u]);
+            Vec<T, VEC>::load(dy + (r + u * rs) * features + col, b[u]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) a[u][e] = b[u][e] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] = fmaf(a[u][e], b[u][e], acc[e]);
+      }
     }
   }
+  // sum the row lanes of each column: tree over the row lanes (fixed order)
 #pragma unroll
   for (int e = 0; e < VEC; ++e) s_s[threadIdx.x * VEC + e] = acc[e];
-  __syncthreads();
-  if (tr == 0) {
+  for (int h = rs >> 1; h >= 1; h >>= 1) {
+    __syncthreads();
+    if (tr < h) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      float t = 0.f;
-      for (int j = 0; j < rs; ++j) t += s_s[(j * ct + tc) * VEC + e];
-      acc[e] = t;
+      for (int e = 0; e < VEC; ++e) {
+        acc[e] += s_s[((tr + h) * ct + tc) * VEC + e];
+        s_s[threadIdx.x * VEC + e] = acc[e];
+      }
     }
   }
   __syncthreads();
@@ -206,6 +327,20 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_bwd_kernel(
   if (!active) return;
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = s_s[tc * VEC + e];
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kSmCacheBwd; ++i) {
+      const int64_t r = start + tr + (int64_t)i * rs;
+      if (r >= end) continue;
+      float a[VEC], b[VEC];
+      hy[i].get(a);
+      hd[i].get(b);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) a[e] = a[e] * (b[e] - acc[e]);
+      Vec<T, VEC>::store(dx + r * features + col, a);
+    }
+    return;
+  }
   for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
     float a[kUnroll][VEC], b[kUnroll][VEC];
 #pragma unroll
@@ -234,16 +369,22 @@ struct SmShape {
   int64_t chunks;
 };
 template <typename T>
-SmShape sm_shape(int64_t features, bool aligned, int batch) {
+SmShape sm_shape(int64_t features, bool aligned, int batch, int64_t total, int threads,
+                 int cache_rows) {
   constexpr int V = 16 / sizeof(T);
   SmShape sh;
   sh.vec = features % V == 0 && aligned;
   const int64_t units = sh.vec ? features / V : features;  // column vectors per row
   sh.ct = 1;
   while (sh.ct < units && sh.ct < 64) sh.ct <<= 1;
-  // fewer column lanes -> more chunks, more workgroups (each row segment a
-  // lane group reads stays >= 8 x 16 bytes contiguous)
-  while (sh.ct > 8 && (int64_t)batch * ((units + sh.ct - 1) / sh.ct) < kSmMinBlocks) sh.ct >>= 1;
+  // Fewer column lanes -> more chunks, more workgroups, and more row lanes,
+  // i.e. longer sequences held in registers: narrow until the grid is large
+  // and cache_rows rows per row lane cover twice the mean sequence length (each
+  // row segment a lane group reads stays >= 8 x 16 bytes contiguous).
+  const int64_t cover = 2 * ((total + batch - 1) / batch);
+  while (sh.ct > 8 && ((int64_t)batch * ((units + sh.ct - 1) / sh.ct) < kSmMinBlocks ||
+                       (int64_t)cache_rows * (threads / sh.ct) < cover))
+    sh.ct >>= 1;
   sh.chunks = (units + sh.ct - 1) / sh.ct;
   return sh;
 }
@@ -252,16 +393,18 @@ template <typename T>
 int launch_softmax_bwd(const void* y, const void* dy, void* dx, const int32_t* cu, int batch,
                        int64_t total, int64_t features, hipStream_t stream) {
   constexpr int V = 16 / sizeof(T);
-  const SmShape sh = sm_shape<T>(features, aligned16(y) && aligned16(dy) && aligned16(dx), batch);
+  const SmShape sh =
+      sm_shape<T>(features, aligned16(y) && aligned16(dy) && aligned16(dx), batch, total,
+                  kSmThreadsBwd, kSmCacheBwd);
   if ((int64_t)batch * sh.chunks > 0x7fffffff)
     return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax_bwd: grid too large");
   const dim3 grid((unsigned)(batch * sh.chunks));
   if (sh.vec)
-    hipLaunchKernelGGL((varlen_softmax_bwd_kernel<T, V>), grid, dim3(kSmThreads), 0, stream,
+    hipLaunchKernelGGL((varlen_softmax_bwd_kernel<T, V>), grid, dim3(kSmThreadsBwd), 0, stream,
                        static_cast<const T*>(y), static_cast<const T*>(dy), static_cast<T*>(dx),
                        cu, total, features, sh.ct, (int)sh.chunks);
   else
-    hipLaunchKernelGGL((varlen_softmax_bwd_kernel<T, 1>), grid, dim3(kSmThreads), 0, stream,
+    hipLaunchKernelGGL((varlen_softmax_bwd_kernel<T, 1>), grid, dim3(kSmThreadsBwd), 0, stream,
                        static_cast<const T*>(y), static_cast<const T*>(dy), static_cast<T*>(dx),
                        cu, total, features, sh.ct, (int)sh.chunks);
   return check_launch("scree_varlen_softmax_bwd");
@@ -271,7 +414,8 @@ template <typename T>
 int launch_softmax(const void* x, void* y, const int32_t* cu, int batch, int64_t total,
                    int64_t features, hipStream_t stream) {
   constexpr int V = 16 / sizeof(T);
-  const SmShape sh = sm_shape<T>(features, aligned16(x) && aligned16(y), batch);
+  const SmShape sh = sm_shape<T>(features, aligned16(x) && aligned16(y), batch, total,
+                                 kSmThreads, kSmCache);
   if ((int64_t)batch * sh.chunks > 0x7fffffff)
     return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: grid too large");
   const dim3 grid((unsigned)(batch * sh.chunks));
