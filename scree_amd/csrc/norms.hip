@@ -48,6 +48,19 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
     const int vi = c * kWave + lane;
     v[c] = vi < nvec ? ld16_nt(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
   }
+  // RMSNorm loads its weight vectors with the row, so their (L2) latency
+  // overlaps the row's instead of following the reduction; LayerNorm, with
+  // the bias too, would lose a wave per SIMD to the registers and keeps the
+  // loads at the output.
+  constexpr bool kEarlyW = !LAYER;
+  uint4 wvs[kEarlyW ? CHUNKS : 1];
+  if constexpr (kEarlyW) {
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int vi = c * kWave + lane;
+      wvs[c] = (w && vi < nvec) ? ld16(w + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+    }
+  }
   if (RES) {
     const T* rr = res + row * (int64_t)dim;
     T* hr = hout + row * (int64_t)dim;
@@ -102,7 +115,10 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
     const int vi = c * kWave + lane;
     if (vi < nvec) {
       uint4 wv = make_uint4(0, 0, 0, 0), bv = make_uint4(0, 0, 0, 0);
-      if (w) wv = ld16(w + (int64_t)vi * VEC);
+      if constexpr (kEarlyW)
+        wv = wvs[c];
+      else if (w)
+        wv = ld16(w + (int64_t)vi * VEC);
       if (LAYER && b) bv = ld16(b + (int64_t)vi * VEC);
       float f[VEC];
 #pragma unroll
