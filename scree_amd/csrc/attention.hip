@@ -394,9 +394,9 @@ struct DmaTile {
   // (ROWS * D elements); rows >= limit become zeros.
   __device__ __forceinline__ void load(T* lds, const T* __restrict__ base, int64_t row_stride,
                                        int row0, int limit, int wave) const {
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS address-space cast exists only on the device side
     const int valid = min(ROWS, limit - row0);
     const uint32_t bytes = valid > 0 ? (uint32_t)((int64_t)valid * row_stride * (int64_t)sizeof(T)) : 0u;
-#if defined(__HIP_DEVICE_COMPILE__)  // the LDS address-space cast exists only on the device side
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)row0 * row_stride, bytes);
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
@@ -404,6 +404,8 @@ struct DmaTile {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rs, (__attribute__((address_space(3))) void*)(lds + q * 512), 16, voff[i], 0, 0, 0);
     }
+#else
+    (void)lds, (void)base, (void)row_stride, (void)row0, (void)limit, (void)wave;
 #endif
   }
 };
@@ -1152,8 +1154,8 @@ inline int attn_head_major(int heads, int tmax) {
 
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
-                  const int32_t* cu, int heads, int kv_heads, const int64_t* st, float scale,
-                  int tmax, const void* ws, hipStream_t stream) {
+                  const int32_t* /*cu: the items carry the bounds*/, int heads, int kv_heads,
+                  const int64_t* st, float scale, int tmax, const void* ws, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
@@ -1167,7 +1169,7 @@ void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* l
 // strides: {dout, q, k, v, o, dq} x {row, head}
 template <typename T, int D, bool C>
 void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
-                     const float* lse, void* dq, float* delta, const int32_t* cu, int heads,
+                     const float* lse, void* dq, float* delta, const int32_t* /*cu*/, int heads,
                      int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                      hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
@@ -1186,7 +1188,7 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
 // strides: {dout, q, k, v, dk, dv} x {row, head}
 template <typename T, int D, bool C>
 void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
-                      const float* lse, const float* delta, void* dk, void* dv, const int32_t* cu,
+                      const float* lse, const float* delta, void* dk, void* dv, const int32_t* /*cu*/,
                       int heads, int kv_heads, const int64_t* st, float scale, int tmax,
                       const void* ws, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * kv_heads;  // one workgroup per (item, K/V head)
