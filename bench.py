@@ -7,8 +7,9 @@ Primary line: causal varlen attention forward +
 backward, fp16, 16 sequences summing to 12160 tokens (log-normal, sigma 0.6,
 rescaled), 16 heads x head_dim 64, synthetic N(0,1) inputs already resident
 in HBM.  One step = tile scheduler + forward (O, LSE) + dQ/Delta pass + dK/dV
-pass into preallocated buffers, captured once in a HIP graph and replayed
-(the eager, call-by-call figure is reported beside it).  ``value`` is real-token causal TFLOP/s
+pass into preallocated buffers.  K steps are replayed from HIP graphs of up
+to 10 consecutive steps (graphs of one step and eager call-by-call launches
+are reported beside it).  ``value`` is real-token causal TFLOP/s
 (4*H*D*sum L(L+1)/2 forward, x3.5 for forward+backward).
 
 Also reported (``secondary``): config 3 forward, config 4 on the reference's
@@ -87,6 +88,48 @@ def _graph_time(fn, reps: int, replays: int) -> float:
     return start.elapsed_time(end) / (replays * reps)
 
 
+def _graph_steps_time(fn, steps: int, chunk: int = 10) -> float:
+    """Average milliseconds of one ``fn`` over exactly ``steps`` calls replayed
+    from HIP graphs that hold up to ``chunk`` consecutive calls each.
+
+    A graph launch has a fixed cost on the host and at the front of the GPU
+    queue (~20 us here), so a loop of small launches is captured a few steps
+    per graph, as a training loop would capture its step.  ``steps // chunk``
+    replays of a ``chunk``-call graph plus one replay of a graph of the
+    remainder run exactly ``steps`` calls between the two HIP events.  Each
+    graph is replayed once untimed first (its upload to the device).
+    """
+    import torch
+
+    chunk = max(1, min(chunk, steps))
+    full, rem = divmod(steps, chunk)
+    fn()
+    torch.cuda.synchronize()
+
+    def capture(n):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(n):
+                fn()
+        return graph
+
+    g_full = capture(chunk) if full else None
+    g_rem = capture(rem) if rem else None
+    for g in (g_full, g_rem):
+        if g is not None:
+            g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(full):
+        g_full.replay()
+    if g_rem is not None:
+        g_rem.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 class AttnCase:
     """Preallocated tensors and the four launches of one attention step."""
 
@@ -140,10 +183,11 @@ class AttnCase:
 def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False, kv_heads=None):
     """One step = scheduler + forward (+ dQ + dK/dV) on preallocated buffers.
 
-    ``ms`` times ``steps`` steps replayed from a HIP graph of one step (HIP
-    events around the replays); ``eager_ms`` times the same steps launched
-    call by call from Python.  Per-kernel times replay a graph of 10 launches
-    of that kernel alone.
+    ``ms`` times ``steps`` steps replayed from HIP graphs of up to 10
+    consecutive steps (HIP events around the replays); ``graph1_ms`` replays
+    a graph of one step ``steps`` times (each step pays a graph launch);
+    ``eager_ms`` times the same steps launched call by call from Python.
+    Per-kernel times replay a graph of 10 launches of that kernel alone.
     """
     import torch
 
@@ -159,10 +203,11 @@ def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False, kv_hea
     end.record()
     torch.cuda.synchronize()
     eager_ms = start.elapsed_time(end) / steps
-    ms = _graph_time(step, 1, steps)
+    graph1_ms = _graph_time(step, 1, steps)
+    ms = _graph_steps_time(step, steps)
     flops = cfg.fwd_flops() * (3.5 if backward else 1.0)
     res = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "eager_ms": eager_ms,
-           "eager_tflops": flops / (eager_ms * 1e-3) / 1e12}
+           "eager_tflops": flops / (eager_ms * 1e-3) / 1e12, "graph1_ms": graph1_ms}
     res["mfma_frac"] = res["tflops"] / PEAK_F16_TFLOPS
     if per_kernel:
         kernels = {"attn_schedule": case.schedule, "attn_fwd": case.fwd}
@@ -286,6 +331,11 @@ def time_autograd_step(cfg, dtype, steps, warmup):
     cu = torch.from_numpy(off).to(dev)
 
     def step():
+        # grads start empty each step, as after optimizer.zero_grad() and as in
+        # the reference's loop, which builds fresh leaves per iteration
+        # (benchmarks/modal_autograd_bench.py:125-131); otherwise backward adds
+        # into .grad (three extra elementwise kernels over q, k and v)
+        q.grad = k.grad = v.grad = None
         out = varlen_attention_hip_autograd(q, k, v, cu, causal=cfg.causal)
         out.backward(do)
 
@@ -412,7 +462,7 @@ def main() -> int:
     log(f"primary: {cfg4.name} lengths={cfg4.lengths}")
     prim, _ = time_attention(cfg4, fp16, args.steps, args.warmup, backward=True, per_kernel=True)
     log(f"primary: {prim['ms']:.4f} ms/step, {prim['tflops']:.1f} TFLOP/s "
-        f"(eager launches: {prim['eager_ms']:.4f} ms/step)")
+        f"(one-step graphs: {prim['graph1_ms']:.4f}, eager launches: {prim['eager_ms']:.4f} ms/step)")
 
     # roofline of the dominant kernel: algorithmic FLOPs it owns / its launch time
     f_fwd = cfg4.fwd_flops()
@@ -435,7 +485,10 @@ def main() -> int:
 
     secondary = {"cfg4_kernels_us": {k: round(v * 1e3, 2) for k, v in kms.items()},
                  "cfg4_eager_launches": {"ms": round(prim["eager_ms"], 4),
-                                         "tflops": round(prim["eager_tflops"], 2)}}
+                                         "tflops": round(prim["eager_tflops"], 2)},
+                 "cfg4_one_step_graphs": {"ms": round(prim["graph1_ms"], 4),
+                                          "tflops": round(cfg4.fwd_flops() * 3.5 / (prim["graph1_ms"] * 1e-3)
+                                                          / 1e12, 2)}}
     if not args.primary_only:
         small = max(3, args.steps // 2)
         cfg3 = workloads.config3()
@@ -507,8 +560,9 @@ def main() -> int:
                          f"rescaled), {cfg4.heads} heads x head_dim {cfg4.head_dim}"),
             "lengths": cfg4.lengths,
             "mfma_frac": round(prim["mfma_frac"], 4),
-            "launch": "one step captured in a HIP graph, replayed K times (eager per-call "
-                      "launches reported in secondary.cfg4_eager_launches)",
+            "launch": "K steps replayed from HIP graphs of up to 10 consecutive steps (graphs of "
+                      "one step: secondary.cfg4_one_step_graphs; eager per-call launches: "
+                      "secondary.cfg4_eager_launches)",
             "parallelism": "single GPU",
         },
         "roofline": roofline,
