@@ -18,10 +18,11 @@ on 4 K/V heads), config 5 (bf16, 32x128) forward+backward, config 2
 RMSNorm / LayerNorm / fused add + RMSNorm forward and backward GB/s, varlen
 softmax forward and backward and packed <-> padded conversions GB/s at the
 config-2 shape, torch's own SDPA on the same GPU for calibration (uniform
-lengths with cfg4's token count), the user-facing autograd step,
-and per-kernel HIP-event timings.  ``roofline`` describes the dominant kernel
-of the primary step; ``cpu_baseline`` times the numpy oracle (the reference's
-einsum call pattern) on a bounded sample of the same workload.
+lengths with cfg4's token count), the user-facing autograd step, config 1
+(the reference's CPU case) on the GPU path, and per-kernel HIP-event
+timings.  ``roofline`` describes the dominant kernel of the primary step;
+``cpu_baseline`` times the numpy oracle (the reference's einsum call
+pattern) on a bounded sample of the same workload.
 """
 
 from __future__ import annotations
@@ -312,6 +313,40 @@ def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup):
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def time_config1_gpu(steps, warmup):
+    """Config 1 (the reference's CPU plumbing case) on the GPU path.
+
+    Config 1 is stated in fp32, which the reference's GPU launcher rejects
+    (``triton/varlen_attention.py:215``: fp16/bf16 only), so attention runs
+    in fp16 on the same lengths and 4 heads x head_dim 32 (causal, forward
+    and forward+backward); RMSNorm runs in fp32 on the packed tokens as
+    (tokens, 128) rows with gamma = 1, the reference's own reshaping
+    (``benchmarks/bench_throughput.py:122``).
+    """
+    import torch
+
+    from scree_amd import workloads
+    from scree_amd.kernels.hip import norms as Nm
+
+    lengths = workloads.config1_lengths()
+    out = {"tokens": int(sum(lengths))}
+    for bwd in (False, True):
+        cfg = workloads.AttnConfig("cfg1_attn_gpu", lengths, 4, 32, "fp16", True, bwd)
+        r, _ = time_attention(cfg, torch.float16, steps, warmup, backward=bwd)
+        out["attn_causal_fp16_fwd_bwd" if bwd else "attn_causal_fp16_fwd"] = {
+            "us": round(r["ms"] * 1e3, 2), "tflops": round(r["tflops"], 3)}
+    dev = torch.device("cuda:0")
+    x = torch.randn(out["tokens"], 128, device=dev, dtype=torch.float32,
+                    generator=torch.Generator(device=dev).manual_seed(3))
+    w = torch.ones(128, device=dev, dtype=torch.float32)
+    for _ in range(warmup):
+        Nm.rmsnorm_fwd(x, w, 1e-6, False)
+    ms = _events_time(lambda: Nm.rmsnorm_fwd(x, w, 1e-6, False), steps)
+    nbytes = workloads.norm_fwd_bytes(out["tokens"], 128, 4, False)
+    out["rmsnorm_fp32_x128_fwd"] = {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    return out
+
+
 def time_autograd_step(cfg, dtype, steps, warmup):
     """User-facing path: autograd Function forward + backward (allocations included)."""
     import numpy as np
@@ -505,6 +540,8 @@ def main() -> int:
             log(f"{name}: {r['ms']:.4f} ms {r['tflops']:.1f} TFLOP/s")
         au = time_autograd_step(cfg4, fp16, args.steps, args.warmup)
         secondary["cfg4_autograd_user_call"] = {"ms": round(au["ms"], 4), "tflops": round(au["tflops"], 2)}
+        secondary["cfg1_gpu"] = time_config1_gpu(args.steps, args.warmup)
+        log(f"cfg1 on the GPU: {secondary['cfg1_gpu']}")
         cfg5 = workloads.config5()
         r, _ = time_attention(cfg5, torch.bfloat16, small, 2, backward=True, per_kernel=True)
         secondary["cfg5_fwd_bwd_bf16"] = {"ms": round(r["ms"], 3), "tflops": round(r["tflops"], 2),
