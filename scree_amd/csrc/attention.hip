@@ -850,20 +850,30 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
 
 // ---------------------------------------------------- backward: dK and dV
 // Per item: 128 keys (32 per wave) loop over blocks of BQ queries.
-//   S = Q K^T, dP = dO V^T (K, V operands in registers; Q, dO from LDS)
+//   S = Q K^T, dP = dO V^T (V operand in registers, K in registers or, at
+//   D = 128, in LDS; Q, dO from LDS)
 //   P = exp(S - LSE), dS = P (dP - Delta)
 //   dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T read transposed from the LDS
 //   tiles; P, dS in registers)
 // Q and dO tiles arrive by DMA into swizzled LDS tiles, as in the forward;
 // each block's LSE and -Delta rows are staged beside them.  Queries past L
 // hold zeros in Q and dO (and LSE = Delta = 0), so they add nothing to dK or
-// dV: no length mask is needed.  D = 128 holds K, V, dK and dV for its keys
-// in registers: at two waves per SIMD (256 registers each) a few values are
-// spilled to scratch, which still beats one wave per SIMD with no spills
-// (config 5's dK/dV pass: 8.5 ms against 9.9 ms).
+// dV: no length mask is needed.  D = 128 runs two waves per SIMD (256
+// registers each); with K, V, dK and dV of its keys all in registers a few
+// values spilled to scratch, and reloading them waited out the next block's
+// in-flight DMA.  With each wave's K rows staged once in LDS instead (32
+// registers fewer, 64 KB of LDS per workgroup: still two per CU) nothing
+// spills: config 5's dK/dV pass 7.4 ms against 8.7 ms.  At D = 64 the same
+// move changes nothing measurable, so K stays in registers there.
 template <int D>
 constexpr int dkv_bq() {
   return D >= 128 ? 32 : 64;
+}
+// Where the score MFMA takes its K operand from: registers (K held for the
+// whole item), or, at D = 128, the wave's 32 K rows staged once in LDS.
+template <int D>
+constexpr bool dkv_k_lds() {
+  return D >= 128;
 }
 
 template <typename T, int D>
@@ -903,7 +913,8 @@ __device__ __forceinline__ void dkv_store_rows(float* rows, int bq, float pl, fl
 // `lcur` holds [LSE*log2(e) | -Delta] of the block's rows.
 template <typename T, int D, bool CAUSAL>
 __device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __restrict__ cur,
-                                          T* __restrict__ nxt, const float* __restrict__ lcur) {
+                                          T* __restrict__ nxt, const float* __restrict__ lcur,
+                                          const T* __restrict__ kl) {
   typedef typename VecT<T>::x8 x8;
   constexpr int BQ = DkvState<T, D>::BQ;
   constexpr int NQT = BQ / 32;
@@ -934,7 +945,12 @@ __device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __
       }
 #pragma unroll
       for (int s = 0; s < D / 16; ++s) {
-        sacc = mfma32(lds_frag16(sQ + 32 * u * D + st.qoff[s]), st.kf[s], sacc);
+        x8 kfr;
+        if constexpr (dkv_k_lds<D>())
+          kfr = lds_frag16(kl + st.qoff[s]);
+        else
+          kfr = st.kf[s];
+        sacc = mfma32(lds_frag16(sQ + 32 * u * D + st.qoff[s]), kfr, sacc);
         pacc = mfma32(lds_frag16(sO + 32 * u * D + st.qoff[s]), st.vf[s], pacc);
       }
       f32x16 pv;
@@ -980,11 +996,11 @@ __device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __
 // load during the block and land in `lnxt` before the closing barrier.
 template <typename T, int D, bool CAUSAL>
 __device__ __forceinline__ void dkv_step(DkvState<T, D>& st, int b, const T* cur, T* nxt,
-                                         const float* lcur, float* lnxt) {
+                                         const float* lcur, float* lnxt, const T* kl) {
   constexpr int BQ = DkvState<T, D>::BQ;
   const bool more = b + 1 < st.nqb;
   if (more && threadIdx.x < BQ) dkv_load_rows(st, st.qbeg + (b + 1) * BQ + (int)threadIdx.x);
-  dkv_block<T, D, CAUSAL>(st, b, cur, nxt, lcur);
+  dkv_block<T, D, CAUSAL>(st, b, cur, nxt, lcur, kl);
   if (more && threadIdx.x < BQ) dkv_store_rows(lnxt, BQ, st.pl, st.pd);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block b + 1 has landed
   __syncthreads();
@@ -1005,7 +1021,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
   // buffers.  One LDS object: with several, the compiler's LDS lowering drops
   // the alias scopes that keep the DMA and the tile reads apart.
   constexpr int ROWS_T = 2 * BQ * (int)(sizeof(float) / sizeof(T));  // one row buffer, in T
-  __shared__ __align__(16) T smem[2 * BUF + 2 * ROWS_T];
+  constexpr int KL = dkv_k_lds<D>() ? kBM * D : 0;  // K rows of the item's keys
+  __shared__ __align__(16) T smem[2 * BUF + 2 * ROWS_T + KL];
   float* sLD0 = reinterpret_cast<float*>(smem + 2 * BUF);
   float* sLD1 = reinterpret_cast<float*>(smem + 2 * BUF + ROWS_T);
 
@@ -1053,23 +1070,34 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
     }
   };
   start_head(hk * group);
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) st.qoff[s] = swz_off<D>(st.lr, 2 * s + st.g);
+  // This wave's K rows in LDS (D = 128): same swizzle as a Q tile, so the
+  // score MFMA reads them with the Q tile's offsets.  Only this wave reads
+  // them, after the barrier at the top of the head loop.
+  T* kl = smem + 2 * BUF + 2 * ROWS_T + 32 * st.wave * D;
   {  // keys past L read row L-1: their results are never stored
     const int64_t tok = start + min(my_k, L - 1);
     const T* krow = k + tok * sk.row + (int64_t)hk * sk.head;
     const T* vrow = v + tok * sv.row + (int64_t)hk * sv.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
-      st.kf[s] = gmem_frag16(krow + 16 * s + 8 * st.g);
+      if constexpr (dkv_k_lds<D>())
+        *reinterpret_cast<uint4*>(kl + st.qoff[s]) =
+            __builtin_bit_cast(uint4, gmem_frag16(krow + 16 * s + 8 * st.g));
+      else
+        st.kf[s] = gmem_frag16(krow + 16 * s + 8 * st.g);
       st.vf[s] = gmem_frag16(vrow + 16 * s + 8 * st.g);
     }
     // Materialize the fragments here, before the barrier: left to itself the
     // compiler sinks these loads into the block loop, where their counter
     // waits then also wait out each block's freshly issued DMA.
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.kf[s]), "+v"(st.vf[s]));
+    for (int s = 0; s < D / 16; ++s) {
+      if constexpr (!dkv_k_lds<D>()) asm volatile("" : "+v"(st.kf[s]));
+      asm volatile("" : "+v"(st.vf[s]));
+    }
   }
-#pragma unroll
-  for (int s = 0; s < D / 16; ++s) st.qoff[s] = swz_off<D>(st.lr, 2 * s + st.g);
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) st.qtr[dt] = swz_tr_off<D>(st.lr, st.g, dt);
 #pragma unroll
@@ -1083,8 +1111,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
     __syncthreads();
     // Unrolled by two so that each call sees its buffers at fixed positions.
     for (int b = 0; b < st.nqb; b += 2) {
-      dkv_step<T, D, CAUSAL>(st, b, bufA, bufB, sLD0, sLD1);
-      if (b + 1 < st.nqb) dkv_step<T, D, CAUSAL>(st, b + 1, bufB, bufA, sLD1, sLD0);
+      dkv_step<T, D, CAUSAL>(st, b, bufA, bufB, sLD0, sLD1, kl);
+      if (b + 1 < st.nqb) dkv_step<T, D, CAUSAL>(st, b + 1, bufB, bufA, sLD1, sLD0, kl);
     }
     // The last step ended with a barrier: both buffers are free again.
     if (++gi == group) break;
