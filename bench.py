@@ -154,7 +154,9 @@ class AttnCase:
         self.lse = torch.empty(n, h, device=dev, dtype=torch.float32)
         self.dq, self.dk, self.dv = (torch.empty_like(t) for t in (self.q, self.k, self.v))
         self.delta = torch.empty(n, h, device=dev, dtype=torch.float32)
-        self.ws = torch.empty(A.workspace_bytes(len(cfg.lengths), n, d), dtype=torch.uint8, device=dev)
+        # room for the grouped-query dK/dV split (just the schedule when hk == h)
+        self.ws = torch.empty(A.bwd_workspace_bytes(len(cfg.lengths), n, h, hk, d), dtype=torch.uint8,
+                              device=dev)
 
     def schedule(self):
         self.A.attention_schedule(self.cu, self.cfg.total, self.cfg.head_dim, self.cfg.causal, self.ws)

@@ -72,6 +72,17 @@ const char* scree_last_error(void);
  * `total_tokens` tokens in all (independent of heads and causality). */
 size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim);
 
+/* Workspace bytes that let the grouped-query backward split each K/V head's
+ * group of query heads over several workgroups (>= scree_attn_workspace_bytes;
+ * equal to it when heads == kv_heads or the grid already fills the GPU).
+ * The schedule occupies the front as before; the rest holds the parts' fp32
+ * dK / dV sums, which a reduce kernel adds up after the dK/dV pass.  scree_attn_bwd_gqa / _bwd_dkv_gqa split
+ * only when given at least this many bytes, else they run one workgroup per
+ * (item, K/V head).  No counterpart in the reference (it has no grouped-query
+ * attention, docs/kernels.md:177). */
+size_t scree_attn_bwd_workspace_bytes_gqa(int batch, int64_t total_tokens, int heads,
+                                          int kv_heads, int head_dim);
+
 /* Build the longest-work-first tile list for `cu_seqlens` into `workspace`.
  * Must precede scree_attn_fwd / scree_attn_bwd with the same cu_seqlens,
  * head_dim and causal flag; the workspace may then be reused by any number of

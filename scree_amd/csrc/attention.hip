@@ -1006,14 +1006,73 @@ __device__ __forceinline__ void dkv_step(DkvState<T, D>& st, int b, const T* cur
   __syncthreads();
 }
 
-template <typename T, int D, bool CAUSAL>
+// Split-group epilogue: this part's fp32 dK / dV sums of the item's 128
+// keys as rows [dK | dV][128][D] (the columns store_row_slice writes), for
+// dkv_reduce_kernel to add up after the pass.
+template <int D>
+__device__ __forceinline__ void dkv_store_partial(const f32x16 (&dk)[D / 32],
+                                                  const f32x16 (&dv)[D / 32],
+                                                  float* __restrict__ rows, int key, int g) {
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int col = 32 * dt + 8 * qd + 4 * g;
+      *reinterpret_cast<float4*>(rows + (int64_t)key * D + col) =
+          make_float4(dk[dt][4 * qd], dk[dt][4 * qd + 1], dk[dt][4 * qd + 2], dk[dt][4 * qd + 3]);
+      *reinterpret_cast<float4*>(rows + (int64_t)(kBM + key) * D + col) =
+          make_float4(dv[dt][4 * qd], dv[dt][4 * qd + 1], dv[dt][4 * qd + 2], dv[dt][4 * qd + 3]);
+    }
+}
+
+// Sum of the parts of one (item, K/V head) in part order (the result does not
+// depend on which part ran first), scaled and rounded into dK / dV rows.  One
+// workgroup per kRedRows keys of a slot, so the grid stays wide when there
+// are few K/V heads.
+constexpr int kRedRows = 16;
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dkv_reduce_kernel(
+    const float* __restrict__ partial, const int32_t* __restrict__ header,
+    const int4* __restrict__ items, int kv_heads, int gsplit, T* __restrict__ dk,
+    T* __restrict__ dv, Strides sdk, Strides sdv, float scale) {
+  constexpr int CHUNKS = kBM / kRedRows;
+  const int slot = blockIdx.x / CHUNKS, chunk = blockIdx.x % CHUNKS;
+  const int item = slot / kv_heads, hk = slot % kv_heads;
+  if (item >= header[0]) return;
+  const int4 it = items[item];
+  const int start = it.z, L = it.w;
+  const int k0 = ((L + kBM - 1) / kBM - 1 - it.y) * kBM;
+  constexpr int C4 = D / 4;
+  const int64_t part_floats = 2 * kBM * D;
+  const float* base = partial + (int64_t)slot * gsplit * part_floats;
+  for (int idx = threadIdx.x; idx < kRedRows * C4; idx += blockDim.x) {
+    const int r = chunk * kRedRows + idx / C4, c = 4 * (idx % C4);
+    if (k0 + r >= L) continue;
+#pragma unroll
+    for (int kind = 0; kind < 2; ++kind) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int p = 0; p < gsplit; ++p) {
+        const float4 x = *reinterpret_cast<const float4*>(
+            base + p * part_floats + (int64_t)(kind * kBM + r) * D + c);
+        acc.x += x.x, acc.y += x.y, acc.z += x.z, acc.w += x.w;
+      }
+      const float mul = kind == 0 ? scale : 1.0f;
+      const Strides sd = kind == 0 ? sdk : sdv;
+      T* dst = (kind == 0 ? dk : dv) + (int64_t)(start + k0 + r) * sd.row + (int64_t)hk * sd.head + c;
+      *reinterpret_cast<uint2*>(dst) =
+          make_uint2(pack2<T>(acc.x * mul, acc.y * mul), pack2<T>(acc.z * mul, acc.w * mul));
+    }
+  }
+}
+
+template <typename T, int D, bool CAUSAL, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
     T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ header,
     const int4* __restrict__ items, int tmax, int head_major, int kv_heads, int group,
     Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk, Strides sdv, float scale,
-    float scale_log2) {
+    float scale_log2, int gsplit, float* __restrict__ partial) {
   constexpr int BQ = dkv_bq<D>();
   constexpr int TILE = BQ * D;
   constexpr int BUF = 2 * TILE;  // Q tile then dO tile
@@ -1026,11 +1085,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
   float* sLD0 = reinterpret_cast<float*>(smem + 2 * BUF);
   float* sLD1 = reinterpret_cast<float*>(smem + 2 * BUF + ROWS_T);
 
-  // One workgroup per (item, K/V head hk); the group's query heads
-  // hk*group .. hk*group + group - 1 are swept one after another and their
-  // contributions accumulate in the dK / dV registers.
-  int item, hk;
-  if (!map_block(kv_heads, tmax, head_major, 1, item, hk) || item >= header[0]) return;
+  // One workgroup per (item, K/V head hk, part): the part's share of the
+  // group's query heads hk*group + [g0, g1) is swept one head after another
+  // and their contributions accumulate in the dK / dV registers.  With
+  // gsplit > 1 parts, each part stores its fp32 sums and dkv_reduce_kernel
+  // adds them up after the pass.
+  int item, hv;
+  if (!map_block(kv_heads * gsplit, tmax, head_major, 1, item, hv) || item >= header[0]) return;
+  const int hk = hv % kv_heads, part = hv / kv_heads;
+  const int g0 = part * group / gsplit, g1 = (part + 1) * group / gsplit;
   const int heads = kv_heads * group;
   const int4 it = items[item];
   const int start = it.z, L = it.w;
@@ -1069,7 +1132,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
       dkv_store_rows(sLD0, BQ, st.pl, st.pd);
     }
   };
-  start_head(hk * group);
+  start_head(hk * group + g0);
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) st.qoff[s] = swz_off<D>(st.lr, 2 * s + st.g);
   // This wave's K rows in LDS (D = 128): same swizzle as a Q tile, so the
@@ -1106,7 +1169,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
     st.dvacc[dt] = zero16();
   }
 
-  for (int gi = 0;;) {
+  for (int gi = g0;;) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     // Unrolled by two so that each call sees its buffers at fixed positions.
@@ -1115,8 +1178,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
       if (b + 1 < st.nqb) dkv_step<T, D, CAUSAL>(st, b + 1, bufB, bufA, sLD1, sLD0, kl);
     }
     // The last step ended with a barrier: both buffers are free again.
-    if (++gi == group) break;
+    if (++gi == g1) break;
     start_head(hk * group + gi);
+  }
+  if constexpr (SPLIT) {
+    dkv_store_partial<D>(st.dkacc, st.dvacc,
+                         partial + (((int64_t)item * kv_heads + hk) * gsplit + part) * (2 * kBM * D),
+                         32 * st.wave + st.lr, st.g);
+    return;
   }
   if (st.wave_live && my_k < L) {
     T* krow = dk + (int64_t)(start + my_k) * sdk.row + (int64_t)hk * sdk.head;
@@ -1174,6 +1243,31 @@ int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, in
   return SCREE_OK;
 }
 
+// Grouped-query dK/dV has one workgroup per (item, K/V head): group times
+// fewer than the other passes.  When that leaves the GPU short of work (fewer
+// than two rounds of ~3 resident workgroups per CU on 256 CUs), each head
+// group is split into equal parts (a divisor of the group: unequal parts
+// leave the largest as the tail) that run as workgroups of their own.
+// Measured on config 4 with 16 query heads (dK/dV pass + reduce): 4 K/V
+// heads in 4 parts 89 us (one part ~146 us, two parts 107 us), 2 K/V heads
+// in 8 parts 86 us (7 unequal parts 131 us), 1 K/V head in 16 parts 86 us.
+constexpr int64_t kDkvSlots = 1536;
+inline int dkv_gsplit(int64_t tmax, int kv_heads, int group) {
+  const int64_t wgs = tmax * kv_heads;
+  if (group < 2 || wgs >= kDkvSlots) return 1;
+  const int64_t want = (kDkvSlots + wgs - 1) / wgs;
+  for (int p = 2; p < group; ++p)
+    if (group % p == 0 && p >= want) return p;
+  return group;
+}
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+// Bytes after the schedule for a split: fp32 dK / dV sums of 128 keys for
+// every (item, K/V head, part).
+inline size_t dkv_split_bytes(int64_t tmax, int kv_heads, int gsplit, int head_dim) {
+  if (gsplit < 2) return 0;
+  return (size_t)tmax * kv_heads * gsplit * 2 * kBM * head_dim * sizeof(float);
+}
+
 // Head-major block order pays off once every XCD has many rounds of items
 // (~64 resident workgroups per XCD): then L2 locality beats cross-head balance.
 inline int attn_head_major(int heads, int tmax) {
@@ -1218,18 +1312,27 @@ template <typename T, int D, bool C>
 void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
                       const float* lse, const float* delta, void* dk, void* dv, const int32_t* /*cu*/,
                       int heads, int kv_heads, const int64_t* st, float scale, int tmax,
-                      const void* ws, hipStream_t stream) {
-  const int64_t grid = (int64_t)tmax * kv_heads;  // one workgroup per (item, K/V head)
+                      const void* ws, int gsplit, float* partial, hipStream_t stream) {
+  // one workgroup per (item, K/V head, part of the head group)
+  const int64_t grid = (int64_t)tmax * kv_heads * gsplit;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
-  hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0,
-                     stream, static_cast<const T*>(dout), static_cast<const T*>(q),
+  // the split epilogue has a kernel of its own: its registers would cost the
+  // unsplit kernel a wave per SIMD at D = 64
+  auto kern = gsplit > 1 ? attn_bwd_dkv_kernel<T, D, C, true> : attn_bwd_dkv_kernel<T, D, C, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                     static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), lse, delta,
                      static_cast<T*>(dk), static_cast<T*>(dv), header, items, tmax,
-                     attn_head_major(kv_heads, tmax), kv_heads, heads / kv_heads,
+                     attn_head_major(kv_heads * gsplit, tmax), kv_heads, heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
-                     scale * kLog2e);
+                     scale * kLog2e, gsplit, partial);
+  if (gsplit > 1)
+    hipLaunchKernelGGL((dkv_reduce_kernel<T, D>),
+                       dim3((unsigned)((int64_t)tmax * kv_heads * (kBM / kRedRows))), dim3(256), 0,
+                       stream, partial, header, items, kv_heads, gsplit, static_cast<T*>(dk),
+                       static_cast<T*>(dv), Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale);
 }
 
 #define SCREE_DISPATCH(FN, dtype, D, causal, ...)                                 \
@@ -1397,10 +1500,31 @@ extern "C" int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const voi
   if (rc) return rc;
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
+  // Split the head groups only when the caller's workspace has room for it
+  // (scree_attn_bwd_workspace_bytes_gqa); otherwise one part per group.
+  int gsplit = dkv_gsplit(tmax, kv_heads, heads / kv_heads);
+  const size_t base = align256(scree_attn_workspace_bytes(batch, total_tokens, head_dim));
+  if (gsplit > 1 && workspace_bytes < base + dkv_split_bytes(tmax, kv_heads, gsplit, head_dim))
+    gsplit = 1;
+  float* partial = gsplit > 1 ? reinterpret_cast<float*>(
+                                    static_cast<char*>(const_cast<void*>(workspace)) + base)
+                              : nullptr;
   SCREE_DISPATCH(launch_bwd_dkv_t, dtype, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
-                 cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace,
-                 static_cast<hipStream_t>(stream));
+                 cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace, gsplit,
+                 partial, static_cast<hipStream_t>(stream));
   return check_launch(fn);
+}
+
+extern "C" size_t scree_attn_bwd_workspace_bytes_gqa(int batch, int64_t total_tokens, int heads,
+                                                     int kv_heads, int head_dim) {
+  const size_t base = scree_attn_workspace_bytes(batch, total_tokens, head_dim);
+  if (!base || kv_heads < 1 || heads < kv_heads || heads % kv_heads ||
+      (head_dim != 32 && head_dim != 64 && head_dim != 128))
+    return base;
+  const int64_t tmax = tmax_for(batch, total_tokens);
+  const int gsplit = dkv_gsplit(tmax, kv_heads, heads / kv_heads);
+  if (gsplit < 2) return base;
+  return align256(base) + dkv_split_bytes(tmax, kv_heads, gsplit, head_dim);
 }
 
 extern "C" int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k, const void* v,

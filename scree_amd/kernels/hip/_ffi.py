@@ -34,6 +34,7 @@ _SIGNATURES = {
     "scree_abi_version": (_I, []),
     "scree_last_error": (ctypes.c_char_p, []),
     "scree_attn_workspace_bytes": (_S, [_I, _L, _I]),
+    "scree_attn_bwd_workspace_bytes_gqa": (_S, [_I, _L, _I, _I, _I]),
     "scree_attn_schedule": (_I, [_P, _I, _L, _I, _I, _P, _S, _P]),
     "scree_attn_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I, _P, _S, _P]),
     "scree_attn_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I,

@@ -71,6 +71,18 @@ def workspace_bytes(batch: int, total: int, head_dim: int) -> int:
     return int(_ffi.lib().scree_attn_workspace_bytes(batch, total, head_dim))
 
 
+def bwd_workspace_bytes(batch: int, total: int, heads: int, kv_heads: int, head_dim: int) -> int:
+    """Workspace bytes for a forward + backward with ``kv_heads`` K/V heads:
+    the schedule, plus room for the grouped-query dK/dV split when it pays."""
+    return int(_ffi.lib().scree_attn_bwd_workspace_bytes_gqa(batch, total, heads, kv_heads,
+                                                             head_dim))
+
+
+def _bwd_workspace(cu_seqlens, total, heads, kv_heads, head_dim):
+    nbytes = bwd_workspace_bytes(cu_seqlens.numel() - 1, total, heads, kv_heads, head_dim)
+    return torch.empty(nbytes, dtype=torch.uint8, device=cu_seqlens.device)
+
+
 def attention_schedule(cu_seqlens: torch.Tensor, total_tokens: int, head_dim: int, causal: bool,
                        workspace: torch.Tensor = None) -> torch.Tensor:
     """Build the device work list for ``cu_seqlens`` and return its workspace.
@@ -213,6 +225,7 @@ def varlen_attention_hip_backward(do, q, k, v, o, lse, cu_seqlens, causal: bool 
     ins = [_kernel_view(t) for t in (do, q, k, v, o)]
     with torch.cuda.device(q.device):
         if workspace is None:
-            workspace = attention_schedule(cu, total, head_dim, causal)
+            workspace = attention_schedule(cu, total, head_dim, causal,
+                                           _bwd_workspace(cu, total, n_heads, k.shape[1], head_dim))
         _attn_bwd(*ins, lse.contiguous(), cu, causal, dq, dk, dv, delta, workspace)
     return dq, dk, dv

@@ -76,6 +76,32 @@ def test_workspace_sizes():
     assert lib.scree_norm_bwd_workspace_bytes(10, 100) == 2 * 2 * 100 * 4
 
 
+def test_grouped_query_backward_workspace_sizes():
+    lib = _ffi.lib()
+    base = lib.scree_attn_workspace_bytes(16, 12160, 64)
+    # equal heads: nothing beyond the schedule
+    assert lib.scree_attn_bwd_workspace_bytes_gqa(16, 12160, 16, 16, 64) == base
+    # 111 items x 4 K/V heads = 444 workgroups < 1536: ceil(1536 / 444) = 4 parts,
+    # a divisor of the group of 4; after the (256-aligned) schedule, fp32 dK and
+    # dV of 128 keys per part
+    tmax, kv, parts = 95 + 16, 4, 4
+    align = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    part = 2 * 128 * 64 * 4
+    want = align(base) + tmax * kv * parts * part
+    assert lib.scree_attn_bwd_workspace_bytes_gqa(16, 12160, 16, 4, 64) == want
+    # 2 K/V heads: ceil(1536 / 222) = 7 -> 8, the next divisor of the group of 8
+    assert lib.scree_attn_bwd_workspace_bytes_gqa(16, 12160, 16, 2, 64) == align(base) + tmax * 2 * 8 * part
+    # 4 K/V heads of 32 query heads: ceil(1536 / 444) = 4, a divisor of 8
+    assert lib.scree_attn_bwd_workspace_bytes_gqa(16, 12160, 32, 4, 64) == align(base) + tmax * 4 * 4 * part
+    # 3 K/V heads of 18: ceil(1536 / 333) = 5 -> 6, the next divisor of the group of 6
+    assert lib.scree_attn_bwd_workspace_bytes_gqa(16, 12160, 18, 3, 64) == align(base) + tmax * 3 * 6 * part
+    # a grid that already fills the GPU: no split
+    big = lib.scree_attn_workspace_bytes(32, 83977, 128)
+    assert lib.scree_attn_bwd_workspace_bytes_gqa(32, 83977, 32, 8, 128) == big
+    # heads that do not group fall back to the schedule's size
+    assert lib.scree_attn_bwd_workspace_bytes_gqa(16, 12160, 16, 3, 64) == base
+
+
 def test_norm_validation_errors():
     lib = _ffi.lib()
     null = ctypes.c_void_p(0)

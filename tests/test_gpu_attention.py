@@ -110,6 +110,48 @@ def test_grouped_query_autograd_matches_launchers():
     assert ka.grad.shape == (n, 2, 64)
 
 
+@pytest.mark.parametrize("heads,kv_heads,dim", [(8, 4, 128), (8, 2, 64), (16, 1, 32)])
+def test_grouped_query_split_dkv_matches_single_pass(heads, kv_heads, dim):
+    """Grouped-query dK/dV with each head group split over several workgroups
+    (workspace sized by bwd_workspace_bytes: here 2, 4 and 16 parts) against
+    the one-workgroup-per-group pass (schedule-only workspace): the same up to
+    fp32 summation order before the final rounding, dQ untouched, and the
+    split result bit-identical run to run."""
+    from scree_amd.kernels.hip import attention as A
+    from scree_amd.kernels.hip import varlen_attention_hip
+
+    lengths = EDGE_LENGTHS
+    n = sum(lengths)
+    say(f"case: split dK/dV H={heads} Hkv={kv_heads} D={dim} N={n} fp16 causal")
+    off, cu = cu_of(lengths)
+    q = randn((n, heads, dim), torch.float16, 21)
+    k = randn((n, kv_heads, dim), torch.float16, 22)
+    v = randn((n, kv_heads, dim), torch.float16, 23)
+    do = randn((n, heads, dim), torch.float16, 24)
+    out, lse = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    small = A.attention_schedule(cu, n, dim, True)
+    big = A.attention_schedule(cu, n, dim, True, A._bwd_workspace(cu, n, heads, kv_heads, dim))
+    assert big.numel() > small.numel()
+
+    def run(ws):
+        dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
+        delta = torch.empty(n, heads, device=q.device, dtype=torch.float32)
+        A._attn_bwd(do, q, k, v, out, lse, cu, True, dq, dk, dv, delta, ws)
+        torch.cuda.synchronize()
+        return dq, dk, dv
+
+    one, split, again = run(small), run(big), run(big)
+    assert torch.equal(one[0], split[0])
+    for name, a, b, c in zip(("dK", "dV"), one[1:], split[1:], again[1:]):
+        assert torch.equal(b, c), f"{name}: split pass not deterministic"
+        diff = (a.float() - b.float()).abs()
+        # one fp16 ulp (2u relative): two fp32 sums on either side of a rounding boundary
+        bound = 2 * UNIT[torch.float16] * torch.maximum(a.float().abs(), b.float().abs()) + 1e-5
+        worst = float((diff - bound).max())
+        say(f"  {name}: max |single - split| = {float(diff.max()):.3e}")
+        assert worst <= 0, f"{name}: split and single pass differ by more than one rounding"
+
+
 def test_single_token_sequences():
     _run_case([1, 1, 1, 1], 3, 64, torch.float16, True)
 
