@@ -78,8 +78,11 @@ size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim)
  * The schedule occupies the front as before; the rest holds the parts' fp32
  * dK / dV sums, which a reduce kernel adds up after the dK/dV pass.  scree_attn_bwd_gqa / _bwd_dkv_gqa split
  * only when given at least this many bytes, else they run one workgroup per
- * (item, K/V head).  No counterpart in the reference (it has no grouped-query
- * attention, docs/kernels.md:177). */
+ * (item, K/V head).  A split backward writes its partial sums into the
+ * workspace, so backward calls that may run at the same time (different
+ * streams) need workspaces of their own; the schedule part is only read.
+ * No counterpart in the reference (it has no grouped-query attention,
+ * docs/kernels.md:177). */
 size_t scree_attn_bwd_workspace_bytes_gqa(int batch, int64_t total_tokens, int heads,
                                           int kv_heads, int head_dim);
 
