@@ -15,7 +15,7 @@ from parity import cu_of, randn, say
 pytestmark = pytest.mark.gpu
 
 
-def _case(lengths, heads, kv_heads, dim, dtype, causal):
+def _case(lengths, heads, kv_heads, dim, dtype, causal, split=False):
     from scree_amd.kernels.hip import attention as A
 
     n = sum(lengths)
@@ -28,7 +28,11 @@ def _case(lengths, heads, kv_heads, dim, dtype, causal):
     t["lse"] = torch.empty(n, heads, device="cuda", dtype=torch.float32)
     t["delta"] = torch.empty(n, heads, device="cuda", dtype=torch.float32)
     t["dq"], t["dk"], t["dv"] = (torch.empty_like(t[x]) for x in ("q", "k", "v"))
-    ws = torch.empty(A.workspace_bytes(len(lengths), n, dim), dtype=torch.uint8, device="cuda")
+    # split: room for the grouped-query dK/dV split (partial sums + reduce kernel)
+    nbytes = (A.bwd_workspace_bytes(len(lengths), n, heads, kv_heads, dim) if split
+              else A.workspace_bytes(len(lengths), n, dim))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    t["ws"] = ws
 
     def step():
         A.attention_schedule(cu, n, dim, causal, ws)
@@ -44,11 +48,15 @@ def _case(lengths, heads, kv_heads, dim, dtype, causal):
 OUTS = ("out", "lse", "delta", "dq", "dk", "dv")
 
 
-@pytest.mark.parametrize("kv_heads", [8, 2])
-def test_graph_replays_match_eager(kv_heads):
+@pytest.mark.parametrize("kv_heads,split", [(8, False), (2, False), (2, True)])
+def test_graph_replays_match_eager(kv_heads, split):
+    from scree_amd.kernels.hip import attention as A
+
     lengths = [300, 17, 129, 640, 1]
-    say(f"case: graph replay lengths={lengths} H=8 Hkv={kv_heads} D=64 fp16 causal")
-    t, step = _case(lengths, 8, kv_heads, 64, torch.float16, True)
+    say(f"case: graph replay lengths={lengths} H=8 Hkv={kv_heads} D=64 fp16 causal split={split}")
+    t, step = _case(lengths, 8, kv_heads, 64, torch.float16, True, split)
+    if split:
+        assert t["ws"].numel() > A.workspace_bytes(len(lengths), sum(lengths), 64)
     step()
     torch.cuda.synchronize()
     want = {k: t[k].clone() for k in OUTS}
@@ -58,6 +66,7 @@ def test_graph_replays_match_eager(kv_heads):
     for rep in range(3):
         for k in OUTS:  # eager work between replays: clobber every output
             t[k].fill_(float("nan"))
+        t["ws"].fill_(255)  # and the workspace: the step rebuilds the schedule
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
