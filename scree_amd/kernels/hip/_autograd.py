@@ -26,9 +26,11 @@ class VarlenAttentionHip(torch.autograd.Function):
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         lse = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
         with torch.cuda.device(q.device):
+            # room for the grouped-query dK/dV split only if a backward can follow
             ws = _attn.attention_schedule(
                 cu, total, head_dim, causal,
-                _attn._bwd_workspace(cu, total, n_heads, k.shape[1], head_dim))
+                _attn._bwd_workspace(cu, total, n_heads, k.shape[1], head_dim)
+                if any(ctx.needs_input_grad[:3]) else None)
             _attn._attn_fwd(qk, kk, vk, cu, causal, out, lse, ws)
         ctx.save_for_backward(qk, kk, vk, out, lse, cu, ws)
         ctx.causal = causal
