@@ -17,7 +17,8 @@ fixed H100 length list, config 4 with grouped-query attention (16 query heads
 on 4 K/V heads), config 5 (bf16, 32x128) forward+backward, config 2
 RMSNorm / LayerNorm / fused add + RMSNorm forward and backward GB/s, varlen
 softmax forward and backward and packed <-> padded conversions GB/s at the
-config-2 shape, torch's own SDPA on the same GPU for calibration (uniform
+config-2 shape, the reference's 27-shape sweep (head_dim x heads x mean
+length, fp16 causal, forward and forward+backward), torch's own SDPA on the same GPU for calibration (uniform
 lengths with cfg4's token count), the user-facing autograd step, config 1
 (the reference's CPU case) on the GPU path, and per-kernel HIP-event
 timings.  ``roofline`` describes the dominant kernel of the primary step;
@@ -349,6 +350,43 @@ def time_config1_gpu(steps, warmup):
     return out
 
 
+def time_shape_sweep(steps, warmup):
+    """The reference's 27-shape sweep (``benchmarks/modal_multishape_sweep.py:64-69``):
+    head_dim 32/64/128 x heads 4/8/16 x mean length 256/1024/2048, 16
+    sequences, log-normal sigma 0.6 (seed 0, ``max(1, int(x))``, no clip),
+    causal fp16.  Each row: forward and forward+backward steps (scheduler
+    included) on preallocated buffers, replayed from HIP graphs of up to 10
+    steps, real-token causal TFLOP/s and fraction of the dense fp16 peak."""
+    import torch
+
+    from scree_amd import workloads
+
+    rows = []
+    for head_dim in (32, 64, 128):
+        for heads in (4, 8, 16):
+            for mean_len in (256, 1024, 2048):
+                lengths = workloads.lognormal_lengths(16, mean_len, 0.6, seed=0, lo=1)
+                cfg = workloads.AttnConfig(f"sweep_d{head_dim}_h{heads}_m{mean_len}", lengths, heads,
+                                           head_dim, "fp16", True, True)
+                case = AttnCase(cfg, torch.float16)
+                row = {"head_dim": head_dim, "heads": heads, "mean_len": mean_len,
+                       "tokens": cfg.total}
+                for tag, step, mult in (("fwd", case.step_fwd, 1.0), ("fwd_bwd", case.step_fwd_bwd, 3.5)):
+                    for _ in range(warmup):
+                        step()
+                    ms = _graph_steps_time(step, steps)
+                    tf = cfg.fwd_flops() * mult / (ms * 1e-3) / 1e12
+                    row[f"{tag}_ms"] = round(ms, 4)
+                    row[f"{tag}_tflops"] = round(tf, 1)
+                    row[f"{tag}_mfma_frac"] = round(tf / PEAK_F16_TFLOPS, 4)
+                rows.append(row)
+                del case
+                log(f"sweep d{head_dim} h{heads} m{mean_len}: fwd {row['fwd_ms']:.4f} ms "
+                    f"{row['fwd_tflops']:.0f} TF/s, fwd+bwd {row['fwd_bwd_ms']:.4f} ms "
+                    f"{row['fwd_bwd_tflops']:.0f} TF/s")
+    return rows
+
+
 def time_autograd_step(cfg, dtype, steps, warmup):
     """User-facing path: autograd Function forward + backward (allocations included)."""
     import numpy as np
@@ -477,6 +515,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the 27-shape sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the varlen "
@@ -567,6 +606,8 @@ def main() -> int:
             "ours_ms": round(ours["ms"], 4), "ours_tflops": round(ours["tflops"], 2),
             "torch_sdpa_ms": round(ref["ms"], 4), "torch_sdpa_tflops": round(ref["tflops"], 2)}
         log(f"calibration 16x760: ours {ours['tflops']:.0f} TF/s, torch SDPA {ref['tflops']:.0f} TF/s")
+        if not args.no_sweep:
+            secondary["reference_shape_sweep_fp16_causal"] = time_shape_sweep(20, 3)
         nr = time_norms(workloads.config2(), args.steps, args.warmup)
         secondary["cfg2_norms_bf16"] = {k: {"us": round(v["ms"] * 1e3, 2), "GB/s": round(v["GB/s"], 1),
                                             "hbm_frac": round(v["hbm_frac"], 4)} for k, v in nr.items()}

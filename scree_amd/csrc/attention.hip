@@ -46,7 +46,8 @@ constexpr float kNegInf = -__builtin_inff();
 // = {seq, blk, start, len}.  start/len are the sequence's offsets clamped to
 // [0, total_tokens], so attention kernels never index outside the tensors
 // even for malformed offsets; if those would make T exceed Tmax the
-// scheduler publishes T = 0 (no work) and header[1] = -1.
+// scheduler publishes T = 0 (no work) and header[1] = -1, and the attention
+// kernels then fill their outputs with NaN (poison_rows).
 constexpr size_t kHeaderBytes = 16;
 
 inline int64_t tmax_for(int batch, int64_t total) { return (total + kBM - 1) / kBM + batch; }
@@ -334,6 +335,22 @@ __device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, i
   return true;
 }
 
+// The scheduler publishes header[1] = -1 when the offsets describe more work
+// than the host bound allows (possible only for offsets that decrease, i.e.
+// overlapping sequences).  Every kernel then fills its outputs with NaN, block
+// b taking token rows b, b + grid, ..., instead of leaving them unwritten.
+template <typename T>
+__device__ __forceinline__ void poison_rows(T* __restrict__ p, Strides s, int total, int heads, int d) {
+  const T nan = from_f32<T>(__builtin_nanf(""));
+  for (int64_t t = blockIdx.x; t < total; t += gridDim.x)
+    for (int i = threadIdx.x; i < heads * d; i += blockDim.x)
+      p[t * s.row + (int64_t)(i / d) * s.head + i % d] = nan;
+}
+__device__ __forceinline__ void poison_stats(float* __restrict__ p, int total, int heads) {
+  for (int64_t t = blockIdx.x; t < total; t += gridDim.x)
+    for (int i = threadIdx.x; i < heads; i += blockDim.x) p[t * heads + i] = __builtin_nanf("");
+}
+
 // A softmax row's reference maximum is raised only when the block maximum
 // exceeds it by more than this many powers of two; p = 2^(s*c - m*c) then
 // stays <= 2^8, which fp32 sums and fp16/bf16 operands hold exactly as well
@@ -571,11 +588,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, const int32_t* __restrict__ header, const int4* __restrict__ items,
     int tmax, int head_major, int heads, int group, Strides sq, Strides sk, Strides sv,
-    Strides so, float scale, float scale_log2) {
+    Strides so, float scale, float scale_log2, int total) {
   constexpr int TILE = kBN * D;  // elements per K or V tile
   constexpr int BUF = 2 * TILE;  // one buffer: K tile then V tile
   __shared__ __align__(16) T smem[2 * BUF];
 
+  if (header[1] < 0) {  // failed schedule
+    poison_rows(o, so, total, heads, D);
+    poison_stats(lse, total, heads);
+    return;
+  }
   int item, h;
   if (!map_block(heads, tmax, head_major, group, item, h) || item >= header[0]) return;
   const int hk = h / group;  // K/V head of this query head
@@ -775,12 +797,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
     float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ header,
     const int4* __restrict__ items, int tmax, int head_major, int heads, int group, Strides sdo,
-    Strides sq, Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2) {
+    Strides sq, Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2,
+    int total) {
   typedef typename VecT<T>::x8 x8;
   constexpr int TILE = kBN * D;
   constexpr int BUF = 2 * TILE;  // K tile then V tile
   __shared__ __align__(16) T smem[dq_nbuf<D>() * BUF];
 
+  if (header[1] < 0) {  // failed schedule
+    poison_rows(dq, sdq, total, heads, D);
+    poison_stats(delta, total, heads);
+    return;
+  }
   int item, h;
   if (!map_block(heads, tmax, head_major, group, item, h) || item >= header[0]) return;
   const int hk = h / group;  // K/V head of this query head
@@ -1065,14 +1093,22 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(
   }
 }
 
+// Waves per SIMD the dK/dV kernel is compiled for: three (168 registers)
+// where that needs no spills -- head_dim 32, and the causal form at 64 --
+// two otherwise.
+template <int D, bool CAUSAL>
+constexpr int dkv_waves() {
+  return D <= 32 || (D == 64 && CAUSAL) ? 3 : 2;
+}
+
 template <typename T, int D, bool CAUSAL, bool SPLIT>
-__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
+__global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_dkv_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
     T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ header,
     const int4* __restrict__ items, int tmax, int head_major, int kv_heads, int group,
     Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk, Strides sdv, float scale,
-    float scale_log2, int gsplit, float* __restrict__ partial) {
+    float scale_log2, int gsplit, float* __restrict__ partial, int total) {
   constexpr int BQ = dkv_bq<D>();
   constexpr int TILE = BQ * D;
   constexpr int BUF = 2 * TILE;  // Q tile then dO tile
@@ -1090,6 +1126,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkv_kernel(
   // and their contributions accumulate in the dK / dV registers.  With
   // gsplit > 1 parts, each part stores its fp32 sums and dkv_reduce_kernel
   // adds them up after the pass.
+  if (header[1] < 0) {  // failed schedule
+    poison_rows(dk, sdk, total, kv_heads, D);
+    poison_rows(dv, sdv, total, kv_heads, D);
+    return;
+  }
   int item, hv;
   if (!map_block(kv_heads * gsplit, tmax, head_major, 1, item, hv) || item >= header[0]) return;
   const int hk = hv % kv_heads, part = hv / kv_heads;
@@ -1277,7 +1318,8 @@ inline int attn_head_major(int heads, int tmax) {
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
                   const int32_t* /*cu: the items carry the bounds*/, int heads, int kv_heads,
-                  const int64_t* st, float scale, int tmax, const void* ws, hipStream_t stream) {
+                  const int64_t* st, float scale, int tmax, const void* ws, int total,
+                  hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
@@ -1285,7 +1327,7 @@ void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* l
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<T*>(o), lse, header, items, tmax, attn_head_major(heads, tmax),
                      heads, heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
-                     Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e);
+                     Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e, total);
 }
 
 // strides: {dout, q, k, v, o, dq} x {row, head}
@@ -1293,7 +1335,7 @@ template <typename T, int D, bool C>
 void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
                      const float* lse, void* dq, float* delta, const int32_t* /*cu*/, int heads,
                      int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
-                     hipStream_t stream) {
+                     int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
   const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
@@ -1304,7 +1346,7 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
                      tmax, attn_head_major(heads, tmax), heads, heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
-                     scale * kLog2e);
+                     scale * kLog2e, total);
 }
 
 // strides: {dout, q, k, v, dk, dv} x {row, head}
@@ -1312,7 +1354,7 @@ template <typename T, int D, bool C>
 void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
                       const float* lse, const float* delta, void* dk, void* dv, const int32_t* /*cu*/,
                       int heads, int kv_heads, const int64_t* st, float scale, int tmax,
-                      const void* ws, int gsplit, float* partial, hipStream_t stream) {
+                      const void* ws, int gsplit, float* partial, int total, hipStream_t stream) {
   // one workgroup per (item, K/V head, part of the head group)
   const int64_t grid = (int64_t)tmax * kv_heads * gsplit;
   const int32_t* header = static_cast<const int32_t*>(ws);
@@ -1327,7 +1369,7 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
                      attn_head_major(kv_heads * gsplit, tmax), kv_heads, heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
-                     scale * kLog2e, gsplit, partial);
+                     scale * kLog2e, gsplit, partial, total);
   if (gsplit > 1)
     hipLaunchKernelGGL((dkv_reduce_kernel<T, D>),
                        dim3((unsigned)((int64_t)tmax * kv_heads * (kBM / kRedRows))), dim3(256), 0,
@@ -1426,7 +1468,7 @@ extern "C" int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, v
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, heads,
-                 kv_heads, strides, softmax_scale, tmax, workspace,
+                 kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
@@ -1464,7 +1506,7 @@ extern "C" int scree_attn_bwd_dq_gqa(const void* dout, const void* q, const void
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
                  cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace,
-                 static_cast<hipStream_t>(stream));
+                 (int)total_tokens, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
@@ -1511,7 +1553,7 @@ extern "C" int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const voi
                               : nullptr;
   SCREE_DISPATCH(launch_bwd_dkv_t, dtype, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
                  cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace, gsplit,
-                 partial, static_cast<hipStream_t>(stream));
+                 partial, (int)total_tokens, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 

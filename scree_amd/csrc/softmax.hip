@@ -80,13 +80,18 @@ struct Held {
 };
 
 // Online (max, sum) update with one exp per element: scale whichever of
-// (sum, new term) is behind.
+// (sum, new term) is behind.  Non-finite input gives what the two-pass
+// formula gives (and torch.softmax): a NaN, or a second +inf, makes the sum
+// NaN; so does a first +inf, whose own term exp(inf - inf) is NaN.  fmaxf
+// ignores a NaN operand, so the NaN is carried in the sum, not the max.
 __device__ __forceinline__ void sm_update(float& m, float& l, float v) {
   const float hi = fmaxf(m, v);
-  const float t = hi == -__builtin_inff()
-                      ? 0.f  // -inf so far: nothing to add (avoids -inf - -inf)
-                      : __builtin_amdgcn_exp2f((fminf(m, v) - hi) * kLog2eSm);
-  l = v > m ? fmaf(l, t, 1.0f) : l + t;
+  float t = hi == -__builtin_inff()
+                ? 0.f  // -inf so far: nothing to add (avoids -inf - -inf)
+                : __builtin_amdgcn_exp2f((fminf(m, v) - hi) * kLog2eSm);
+  if (v != v) t = v;  // NaN input: poison the sum
+  const float self = v == __builtin_inff() ? __builtin_nanf("") : 1.0f;  // exp(v - v)
+  l = v > m ? fmaf(l, t, self) : l + t;
   m = hi;
 }
 
@@ -98,11 +103,13 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
   return r;
 }
 
-// Merge the partial (max, sum) of another row lane into (m, l).
+// Merge the partial (max, sum) of another row lane into (m, l).  A lane that
+// has seen only -inf and NaN keeps m = -inf with a NaN sum: l * 0 carries it
+// (0 * 0 = 0 otherwise), and two +inf maxima give exp(inf - inf) = NaN.
 __device__ __forceinline__ void sm_merge(float& m, float& l, float m2, float l2) {
   const float hi = fmaxf(m, m2);
-  const float a = m == -__builtin_inff() ? 0.f : l * __builtin_amdgcn_exp2f((m - hi) * kLog2eSm);
-  const float b = m2 == -__builtin_inff() ? 0.f : l2 * __builtin_amdgcn_exp2f((m2 - hi) * kLog2eSm);
+  const float a = m == -__builtin_inff() ? l * 0.f : l * __builtin_amdgcn_exp2f((m - hi) * kLog2eSm);
+  const float b = m2 == -__builtin_inff() ? l2 * 0.f : l2 * __builtin_amdgcn_exp2f((m2 - hi) * kLog2eSm);
   l = a + b;
   m = hi;
 }

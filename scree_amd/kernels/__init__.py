@@ -37,6 +37,10 @@ def varlen_attention(q: Array, k: Array, v: Array, causal: bool = False) -> Arra
             raise ValueError("q, k, v must have identical offsets")
     if q.ragged_dim != 0:
         raise NotImplementedError("varlen_attention supports ragged_dim=0 only")
+    # Array checks only the two ends; overlapping sequences would give the
+    # scheduler more work than its bound (the kernels then write NaN)
+    if bool((q.offsets[1:] < q.offsets[:-1]).any()):
+        raise ValueError("offsets must be non-decreasing")
     out = varlen_attention_hip_autograd(q.values, k.values, v.values, q.offsets, causal)
     return Array(values=out, offsets=q.offsets, ragged_dim=0)
 

@@ -5,8 +5,11 @@ Mirrors ``varlen_attention_triton_autograd``
 ``(q, k, v, out, lse, cu_seqlens)`` and backward returns ``(dq, dk, dv, None,
 None)``.  Two differences: the Function class is defined once at import
 (the reference rebuilds it on every call, ``_autograd.py:71``), and the
-forward also keeps the device work list it built, so the backward launches
-no scheduler and never synchronises the host.
+forward also keeps the device work list it built (schedule-sized: 16 bytes
+per 128-token block plus 16 per sequence), so the backward launches no
+scheduler and never synchronises the host.  When the grouped-query dK/dV
+split pays, the backward allocates the larger workspace it needs for the
+duration of the pass and copies the work list into it on the device.
 """
 
 from __future__ import annotations
@@ -26,11 +29,7 @@ class VarlenAttentionHip(torch.autograd.Function):
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         lse = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
         with torch.cuda.device(q.device):
-            # room for the grouped-query dK/dV split only if a backward can follow
-            ws = _attn.attention_schedule(
-                cu, total, head_dim, causal,
-                _attn._bwd_workspace(cu, total, n_heads, k.shape[1], head_dim)
-                if any(ctx.needs_input_grad[:3]) else None)
+            ws = _attn.attention_schedule(cu, total, head_dim, causal)
             _attn._attn_fwd(qk, kk, vk, cu, causal, out, lse, ws)
         ctx.save_for_backward(qk, kk, vk, out, lse, cu, ws)
         ctx.causal = causal
@@ -46,6 +45,11 @@ class VarlenAttentionHip(torch.autograd.Function):
         total, n_heads, _ = q.shape
         delta = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
         with torch.cuda.device(q.device):
+            need = _attn.bwd_workspace_bytes(cu.numel() - 1, total, n_heads, k.shape[1], q.shape[2])
+            if need > ws.numel():  # grouped-query split: work list + fp32 partials
+                big = torch.empty(need, dtype=torch.uint8, device=q.device)
+                big[:ws.numel()].copy_(ws)
+                ws = big
             _attn._attn_bwd(do, q, k, v, out, lse, cu, ctx.causal, dq, dk, dv, delta, ws)
         return dq, dk, dv, None, None
 

@@ -46,12 +46,23 @@ def _check_inputs(q, k, v):
     assert q.dim() == 3, "q, k, v must be (total_tokens, n_heads, head_dim)"
 
 
+# Row and head strides the kernels index with 32-bit element offsets.
+_MAX_STRIDE = 1 << 24
+
+
 def _kernel_view(t: torch.Tensor) -> torch.Tensor:
-    """``t`` itself when the library can read it in place, else a contiguous copy."""
+    """``t`` itself when the library can read it in place, else a contiguous copy.
+
+    In place means: head_dim contiguous, row and head strides non-negative
+    multiples of 8 elements below 2^24, a 16-byte aligned base, and rows that
+    do not overlap -- exactly what ``check_tensor`` in the library accepts.
+    """
     ok = (
         t.stride(2) == 1
         and t.stride(0) % 8 == 0
         and t.stride(1) % 8 == 0
+        and 0 <= t.stride(0) < _MAX_STRIDE
+        and 0 <= t.stride(1) < _MAX_STRIDE
         and t.data_ptr() % 16 == 0
         and (t.shape[0] <= 1 or t.stride(0) >= t.shape[2])
     )
@@ -217,11 +228,19 @@ def varlen_attention_hip_backward(do, q, k, v, o, lse, cu_seqlens, causal: bool 
     total, n_heads, head_dim = q.shape
     assert lse.shape == (total, n_heads) and lse.dtype == torch.float32
     cu = _cu(cu_seqlens, q.device)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    delta = delta_buffer if delta_buffer is not None else torch.empty(
-        (total, n_heads), dtype=torch.float32, device=q.device)
+    # fresh, contiguous gradients (empty_like would copy a view's strides)
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if delta_buffer is None:
+        delta = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
+    else:
+        # the dQ kernel writes fp32 Delta at contiguous (token, head) offsets
+        assert delta_buffer.shape == (total, n_heads), "delta_buffer must be (total_tokens, n_heads)"
+        assert delta_buffer.dtype == torch.float32, "delta_buffer must be float32"
+        assert delta_buffer.device == q.device, "delta_buffer must be on q's device"
+        assert delta_buffer.is_contiguous(), "delta_buffer must be contiguous"
+        delta = delta_buffer
     ins = [_kernel_view(t) for t in (do, q, k, v, o)]
     with torch.cuda.device(q.device):
         if workspace is None:

@@ -75,11 +75,17 @@ def attn_abs_terms(q, k, v, do, lse, off, causal):
 
 
 def check_close(name, got, want, atol, extra=None, unit=0.0):
-    """Assert |got - want| <= atol + unit * extra (elementwise); print the figures."""
+    """Assert |got - want| <= atol + unit * extra (elementwise); print the figures.
+
+    The printed line also says whether the flat bound ``atol`` alone holds
+    (``flat=met``), which for bf16 is reported beside the widened bound.
+    """
     err = np.abs(got - want)
     bound = atol + (unit * extra if extra is not None else 0.0)
     worst = float((err - bound).max()) if err.size else 0.0
-    say(f"  {name}: max_abs={float(err.max()) if err.size else 0.0:.3e} "
-        f"(atol {atol:g}{' + u*terms' if extra is not None else ''}) margin={-worst:.3e}")
+    max_abs = float(err.max()) if err.size else 0.0
+    say(f"  {name}: max_abs={max_abs:.3e} "
+        f"(atol {atol:g}{' + u*terms' if extra is not None else ''}) margin={-worst:.3e} "
+        f"flat={'met' if max_abs <= atol else 'exceeded'}")
     assert worst <= 0.0, f"{name}: exceeds tolerance by {worst:.3e}"
-    return float(err.max()) if err.size else 0.0
+    return max_abs

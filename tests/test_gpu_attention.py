@@ -108,6 +108,13 @@ def test_grouped_query_autograd_matches_launchers():
     assert torch.equal(out.detach(), o2)
     assert torch.equal(qa.grad, dq) and torch.equal(ka.grad, dk) and torch.equal(va.grad, dv)
     assert ka.grad.shape == (n, 2, 64)
+    # the forward keeps only the schedule between the passes; this shape takes
+    # the split dK/dV path, whose larger workspace lives only during backward
+    from scree_amd.kernels.hip import attention as A
+    out2 = varlen_attention_hip_autograd(qa, ka, va, cu, causal=True)
+    saved_ws = out2.grad_fn.saved_tensors[-1]
+    assert saved_ws.numel() == A.workspace_bytes(len(lengths), n, 64)
+    assert A.bwd_workspace_bytes(len(lengths), n, 8, 2, 64) > saved_ws.numel()
 
 
 @pytest.mark.parametrize("heads,kv_heads,dim", [(8, 4, 128), (8, 2, 64), (16, 1, 32)])
@@ -165,9 +172,10 @@ def test_config3_fixed_list_fp16_causal():
     _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=3)
 
 
-def test_config3_rescaled_lengths_fp16_causal():
-    c = workloads.config3()
-    _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=4, backward=False)
+def test_config4_rescaled_lengths_fp16_causal_fwd_bwd():
+    """The bench's own workload: config 3/4's rescaled length list, forward and backward."""
+    c = workloads.config4()
+    _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=4, backward=True)
 
 
 def test_config5_sampled_heads_bf16():

@@ -78,6 +78,39 @@ def test_rows_sum_to_one_and_masked_entries():
     assert torch.isnan(torch.softmax(x[10:11].cpu(), dim=0)).all()
 
 
+@pytest.mark.parametrize("length", [300, 5000])
+def test_non_finite_inputs_match_two_pass_semantics(length):
+    """NaN, +inf and all -inf columns give what the max-subtracted two-pass
+    formula (the oracle, pinned to torch.softmax) gives: NaN throughout the
+    affected column.  5000 rows of 8 fp32 columns exceed what the forward keeps
+    in registers (16 rows per row lane, 128 row lanes), so the online update
+    and the row-lane merge see the non-finite values; 300 rows stay cached."""
+    from scree_amd.kernels.hip import varlen_softmax_hip
+
+    say(f"case: non-finite softmax length {length}")
+    lengths = [length, 7]
+    off, cu = cu_of(lengths)
+    x = randn((sum(lengths), 8), torch.float32, 31)
+    x[length // 3, 1] = float("nan")
+    x[length - 2, 2] = float("inf")
+    x[5, 3] = float("inf")
+    x[length // 2, 3] = float("inf")                  # two +inf in one column
+    x[:length, 4] = float("-inf")                      # a column with no finite value
+    x[7, 5] = float("nan")
+    x[:length, 5][x[:length, 5] == x[:length, 5]] = float("-inf")  # only -inf and one NaN
+    x[:length, 6] = float("-inf")
+    x[length - 1, 6] = 1.0                             # one finite value among -inf
+    y = varlen_softmax_hip(x, cu)
+    torch.cuda.synchronize()
+    want = varlen_softmax(np64(x), off)
+    got = np64(y)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    check_close("y (finite entries)", got[fin], want[fin], 1e-5)
+    assert np.isnan(got[:length, 1:6]).all()
+    assert got[length - 1, 6] == 1.0
+
+
 def test_non_contiguous_view():
     from scree_amd.kernels.hip import varlen_softmax_hip
 

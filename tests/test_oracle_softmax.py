@@ -80,3 +80,18 @@ def test_planted_mistake_is_caught():
     off = offsets_from_lengths([2, 4])
     wrong = varlen_softmax(x, offsets_from_lengths([6]))
     assert not np.allclose(wrong, varlen_softmax(x, off))
+
+
+def test_non_finite_columns_match_torch():
+    """NaN, one or two +inf, all -inf, and -inf beside one finite value: the
+    oracle's NaN pattern and finite values are torch.softmax's."""
+    inf, nan = np.inf, np.nan
+    cols = [[0.5, nan, 2.0, -1.0], [1.0, inf, 0.0, 3.0], [inf, 1.0, inf, 0.0],
+            [-inf, -inf, -inf, -inf], [-inf, 4.0, -inf, -inf], [-inf, nan, -inf, -inf]]
+    x = np.array(cols, dtype=np.float64).T  # 4 rows, 6 columns: one sequence
+    off = offsets_from_lengths([4])
+    got = varlen_softmax(x, off)
+    want = torch.softmax(torch.from_numpy(x), dim=0).numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_allclose(got[~np.isnan(want)], want[~np.isnan(want)], rtol=1e-15)
+    assert np.isnan(got[:, [0, 1, 2, 3, 5]]).all() and got[1, 4] == 1.0
