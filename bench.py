@@ -516,6 +516,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-sweep", action="store_true", help="skip the 27-shape sweep")
+    ap.add_argument("--only", choices=["cfg5"], default=None,
+                    help="time one secondary workload alone and print its figures (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the varlen "
@@ -533,6 +535,15 @@ def main() -> int:
     _ffi.lib()  # raise now if the library is missing
     torch.cuda.set_device(0)
     fp16 = torch.float16
+    if args.only == "cfg5":
+        cfg5 = workloads.config5()
+        r, _ = time_attention(cfg5, torch.bfloat16, args.steps, args.warmup, backward=True,
+                              per_kernel=True)
+        print(json.dumps({"workload": cfg5.name, "ms": round(r["ms"], 4), "tflops": round(r["tflops"], 2),
+                          "mfma_frac": round(r["mfma_frac"], 4),
+                          "kernels_us": {k: round(v * 1e3, 1) for k, v in r["kernels_ms"].items()}}),
+              flush=True)
+        return 0
 
     cfg4 = workloads.config4()
     log(f"primary: {cfg4.name} lengths={cfg4.lengths}")

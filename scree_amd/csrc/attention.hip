@@ -257,6 +257,50 @@ __device__ __forceinline__ void store_row_slice(T* row_ptr, int d0, int g, const
   }
 }
 
+// Row-contiguous stores of a wave's 32 result rows, staged through LDS.
+// store_row_slice writes each lane's 4-element runs straight to memory: one
+// instruction then touches 32 rows x 16 bytes, and under the attention
+// kernels' load such scattered stores take microseconds just to issue.  Here
+// the wave writes its accumulators (store_row_slice's layout, scaled by the
+// lane's `mul`) into a wave-private LDS area of 32 rows x (D + 8) elements
+// (the pad spreads the rows over the banks), then reads it back so that lane
+// l holds 16-byte chunk l % CPR of row l / CPR (+ 64 / CPR per round), and
+// CPR lanes store one contiguous row.  Rows >= nrows are not stored.  LDS
+// accesses of one wave are processed in order, so the read-back sees the
+// writes without a workgroup barrier; the caller guarantees no other wave
+// uses `stage` meanwhile.
+constexpr int kStagePad = 8;
+template <int D>
+constexpr int stage_elems() {
+  return 32 * (D + kStagePad);
+}
+template <typename T, int D>
+__device__ __forceinline__ void store_rows_staged(T* __restrict__ stage, const f32x16 (&acc)[D / 32],
+                                                  float mul, T* __restrict__ dst, int64_t row_stride,
+                                                  int nrows, int lr, int g, int lane) {
+  constexpr int SD = D + kStagePad;
+  constexpr int CPR = D / 8;       // 16-byte chunks per row
+  constexpr int RPR = 64 / CPR;    // rows per read round
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const uint32_t lo = pack2<T>(acc[dt][4 * qd + 0] * mul, acc[dt][4 * qd + 1] * mul);
+      const uint32_t hi = pack2<T>(acc[dt][4 * qd + 2] * mul, acc[dt][4 * qd + 3] * mul);
+      *reinterpret_cast<uint2*>(stage + lr * SD + 32 * dt + 8 * qd + 4 * g) = make_uint2(lo, hi);
+    }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int c = lane % CPR;
+#pragma unroll
+  for (int j = 0; j < 32 / RPR; ++j) {
+    const int r = lane / CPR + RPR * j;
+    const uint4 v = *reinterpret_cast<const uint4*>(stage + r * SD + 8 * c);
+    if (r < nrows) *reinterpret_cast<uint4*>(dst + (int64_t)r * row_stride + 8 * c) = v;
+  }
+}
+
 // 2^x on the hardware unit (v_exp_f32); results below 2^-126 may flush to 0,
 // which softmax weights tolerate.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -592,6 +636,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   constexpr int TILE = kBN * D;  // elements per K or V tile
   constexpr int BUF = 2 * TILE;  // one buffer: K tile then V tile
   __shared__ __align__(16) T smem[2 * BUF];
+  static_assert(4 * stage_elems<D>() <= 2 * BUF, "O staging must fit in the tile buffers");
 
   if (header[1] < 0) {  // failed schedule
     poison_rows(o, so, total, heads, D);
@@ -657,14 +702,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     fwd_block<T, D, CAUSAL>(st, kb, bufA, bufB);
     if (kb + 1 < st.nkb) fwd_block<T, D, CAUSAL>(st, kb + 1, bufB, bufA);
   }
-  if (wave_live && my_q < L) {
+  if (wave_live) {  // the last block's barrier freed the tile buffers: stage O there
     const float l_tot = halves_sum(st.l_run);
     const float inv_l = 1.0f / l_tot;
-    T* orow = o + (int64_t)(start + my_q) * so.row + (int64_t)h * so.head;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-      store_row_slice<T>(orow, 32 * dt, st.g, st.oacc[dt], inv_l);
-    if (st.g == 0) lse[(int64_t)(start + my_q) * heads + h] = st.m_run * scale + logf(l_tot);
+    store_rows_staged<T, D>(smem + st.wave * stage_elems<D>(), st.oacc, inv_l,
+                            o + (int64_t)(start + st.qw0) * so.row + (int64_t)h * so.head, so.row,
+                            min(32, L - st.qw0), st.lr, st.g, lane);
+    if (st.g == 0 && my_q < L)
+      lse[(int64_t)(start + my_q) * heads + h] = st.m_run * scale + logf(l_tot);
   }
 }
 
@@ -750,27 +795,32 @@ __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __r
     barrier_vm<0>();
 }
 
-// The dQ block loop over tile buffers A, B (and C): stages blocks 0 (and 1),
-// runs `setup` while they fly, then loops.  Every DMA and tile read sits in
-// this one function, so the compiler's alias scopes tell each pending DMA
+// The dQ block loop over tile buffers A, B (and C): `issue` starts this
+// wave's row loads, then blocks 0 (and 1) are staged, `setup` consumes the
+// rows while the tiles fly, then the loop runs.  The row loads go first:
+// loads retire in order, so rows requested after 32 KB of tile DMA would
+// wait for all of it (microseconds under load).  Every DMA and tile read sits
+// in this one function, so the compiler's alias scopes tell each pending DMA
 // apart from the reads of the other buffers (a DMA pending across two calls
 // of dq_block would otherwise make it wait for the DMA before every read).
-template <typename T, int D, bool CAUSAL, typename Setup>
+template <typename T, int D, bool CAUSAL, typename Issue, typename Setup>
 __device__ __forceinline__ void dq_run(DqState<T, D>& st, T* __restrict__ A, T* __restrict__ B,
-                                       T* __restrict__ C, Setup setup) {
+                                       T* __restrict__ C, Issue issue, Setup setup) {
   constexpr int TILE = kBN * D;
   constexpr int NL = 2 * DmaTile<T, D, kBN>::PER_WAVE;
   constexpr bool three = dq_nbuf<D>() == 3;
+  issue();
   st.dK.load(A, st.kh, st.krow, 0, st.L, st.wave);
   st.dV.load(A + TILE, st.vh, st.vrow, 0, st.L, st.wave);
-  if (three && st.nkb > 1) {
+  if (three) {  // block 1 even when unused (nkb == 1 only for L <= 64): a fixed count
     st.dK.load(B, st.kh, st.krow, kBN, st.L, st.wave);
     st.dV.load(B + TILE, st.vh, st.vrow, kBN, st.L, st.wave);
   }
   setup();
-  // The count is safe with setup's own loads and stores in flight: they can
-  // only add to it, and loads retire in order.
-  if (three && st.nkb > 1)
+  // Block 0 has landed once at most NL operations are younger than it (block
+  // 1's, or fewer when setup's own stores are among them: waiting longer is
+  // only conservative).
+  if (three)
     barrier_vm<NL>();
   else
     barrier_vm<0>();
@@ -803,6 +853,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   constexpr int TILE = kBN * D;
   constexpr int BUF = 2 * TILE;  // K tile then V tile
   __shared__ __align__(16) T smem[dq_nbuf<D>() * BUF];
+  static_assert(4 * stage_elems<D>() <= dq_nbuf<D>() * BUF, "dQ staging must fit in the tile buffers");
 
   if (header[1] < 0) {  // failed schedule
     poison_rows(dq, sdq, total, heads, D);
@@ -834,28 +885,34 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   st.dK.init(sk.row, st.wave, lane);
   st.dV.init(sv.row, st.wave, lane);
 
-  // This wave's query rows, Delta and fragment offsets, set up while the
-  // first K/V blocks are in flight.
+  // This wave's query rows (issued before the first K/V blocks), then Delta
+  // and the fragment offsets, set up while those blocks are in flight.  Rows
+  // past L read row L-1: their results are never stored.
+  x8 of[D / 16];
+  float lse_raw;
+  auto issue = [&] {
+    const int64_t tok = start + min(my_q, L - 1);
+    const T* qrow = q + tok * sq.row + (int64_t)h * sq.head;
+    const T* drow = dout + tok * sdo.row + (int64_t)h * sdo.head;
+    const T* orow = o + tok * so.row + (int64_t)h * so.head;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
+      st.df[s] = gmem_frag16(drow + 16 * s + 8 * st.g);
+      of[s] = gmem_frag16(orow + 16 * s + 8 * st.g);
+    }
+    lse_raw = lse[tok * heads + h];
+  };
   auto setup = [&] {
     float dl = 0.f;
-    {  // rows past L read row L-1: their results are never stored
-      const int64_t tok = start + min(my_q, L - 1);
-      const T* qrow = q + tok * sq.row + (int64_t)h * sq.head;
-      const T* drow = dout + tok * sdo.row + (int64_t)h * sdo.head;
-      const T* orow = o + tok * so.row + (int64_t)h * so.head;
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
-        st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
-        st.df[s] = gmem_frag16(drow + 16 * s + 8 * st.g);
-        const x8 of = gmem_frag16(orow + 16 * s + 8 * st.g);
+    for (int s = 0; s < D / 16; ++s)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dl += (float)of[j] * (float)st.df[s][j];
-      }
-      st.lse2 = lse[tok * heads + h] * kLog2e;
-      // Materialize the fragments before the barrier (see the forward).
+      for (int j = 0; j < 8; ++j) dl += (float)of[s][j] * (float)st.df[s][j];
+    st.lse2 = lse_raw * kLog2e;
+    // Materialize the fragments before the barrier (see the forward).
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.qf[s]), "+v"(st.df[s]));
-    }
+    for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(st.qf[s]), "+v"(st.df[s]));
     dl = halves_sum(dl);
     if (my_q < L && st.g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
 #pragma unroll
@@ -868,12 +925,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     for (int dt = 0; dt < D / 32; ++dt) st.dqacc[dt] = zero16();
     st.scale_log2 = scale_log2;
   };
-  dq_run<T, D, CAUSAL>(st, smem, smem + BUF, dq_nbuf<D>() == 3 ? smem + 2 * BUF : nullptr, setup);
-  if (wave_live && my_q < L) {
-    T* out = dq + (int64_t)(start + my_q) * sdq.row + (int64_t)h * sdq.head;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) store_row_slice<T>(out, 32 * dt, st.g, st.dqacc[dt], scale);
-  }
+  dq_run<T, D, CAUSAL>(st, smem, smem + BUF, dq_nbuf<D>() == 3 ? smem + 2 * BUF : nullptr, issue,
+                       setup);
+  if (wave_live)  // the last block's barrier freed the tile buffers: stage dQ there
+    store_rows_staged<T, D>(smem + st.wave * stage_elems<D>(), st.dqacc, scale,
+                            dq + (int64_t)(start + st.qw0) * sdq.row + (int64_t)h * sdq.head,
+                            sdq.row, min(32, L - st.qw0), st.lr, st.g, lane);
 }
 
 // ---------------------------------------------------- backward: dK and dV
@@ -1118,6 +1175,7 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   constexpr int ROWS_T = 2 * BQ * (int)(sizeof(float) / sizeof(T));  // one row buffer, in T
   constexpr int KL = dkv_k_lds<D>() ? kBM * D : 0;  // K rows of the item's keys
   __shared__ __align__(16) T smem[2 * BUF + 2 * ROWS_T + KL];
+  static_assert(4 * stage_elems<D>() <= 2 * BUF + KL, "dK/dV staging must fit in the tile buffers");
   float* sLD0 = reinterpret_cast<float*>(smem + 2 * BUF);
   float* sLD1 = reinterpret_cast<float*>(smem + 2 * BUF + ROWS_T);
 
@@ -1228,14 +1286,15 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
                          32 * st.wave + st.lr, st.g);
     return;
   }
-  if (st.wave_live && my_k < L) {
-    T* krow = dk + (int64_t)(start + my_k) * sdk.row + (int64_t)hk * sdk.head;
-    T* vrow = dv + (int64_t)(start + my_k) * sdv.row + (int64_t)hk * sdv.head;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-      store_row_slice<T>(krow, 32 * dt, st.g, st.dkacc[dt], scale);
-      store_row_slice<T>(vrow, 32 * dt, st.g, st.dvacc[dt], 1.0f);
-    }
+  if (st.wave_live) {  // the last step's barrier freed the tile buffers: stage dK, then dV
+    const int nrows = min(32, L - st.kw0);
+    T* stage = smem + st.wave * stage_elems<D>();
+    store_rows_staged<T, D>(stage, st.dkacc, scale,
+                            dk + (int64_t)(start + st.kw0) * sdk.row + (int64_t)hk * sdk.head,
+                            sdk.row, nrows, st.lr, st.g, lane);
+    store_rows_staged<T, D>(stage, st.dvacc, 1.0f,
+                            dv + (int64_t)(start + st.kw0) * sdv.row + (int64_t)hk * sdv.head,
+                            sdv.row, nrows, st.lr, st.g, lane);
   }
 }
 
