@@ -27,6 +27,8 @@
 // the same two 4-key runs as A), P never leaves registers.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace scree {
@@ -1505,13 +1507,10 @@ static int check_bwd_tensors(const char* fn, const char* const* names, const voi
   return SCREE_OK;
 }
 
-extern "C" int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
-                                  float* lse, const int32_t* cu_seqlens, int batch,
-                                  int64_t total_tokens, int heads, int kv_heads, int head_dim,
-                                  const int64_t* strides, float softmax_scale, int causal,
-                                  int dtype, const void* workspace, size_t workspace_bytes,
-                                  void* stream) {
-  const char* fn = "scree_attn_fwd";
+static int check_fwd(const char* fn, const void* q, const void* k, const void* v, const void* o,
+                     const float* lse, const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                     int heads, int kv_heads, int head_dim, const int64_t* strides, int dtype,
+                     const void* workspace, size_t workspace_bytes) {
   int rc = check_common(fn, cu_seqlens, batch, total_tokens, heads, head_dim, dtype, workspace,
                         workspace_bytes);
   if (rc) return rc;
@@ -1524,12 +1523,99 @@ extern "C" int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, v
     rc = check_tensor(fn, names[i], ptrs[i], strides + 2 * i, heads, head_dim, total_tokens);
     if (rc) return rc;
   }
+  return SCREE_OK;
+}
+
+static int launch_fwd(const char* fn, const void* q, const void* k, const void* v, void* o,
+                      float* lse, const int32_t* cu_seqlens, int batch, int64_t total_tokens,
+                      int heads, int kv_heads, int head_dim, const int64_t* strides,
+                      float softmax_scale, int causal, int dtype, const void* workspace,
+                      void* stream) {
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, heads,
                  kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
+}
+
+extern "C" int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
+                                  float* lse, const int32_t* cu_seqlens, int batch,
+                                  int64_t total_tokens, int heads, int kv_heads, int head_dim,
+                                  const int64_t* strides, float softmax_scale, int causal,
+                                  int dtype, const void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  const char* fn = "scree_attn_fwd";
+  int rc = check_fwd(fn, q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, kv_heads,
+                     head_dim, strides, dtype, workspace, workspace_bytes);
+  if (rc) return rc;
+  return launch_fwd(fn, q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, kv_heads,
+                    head_dim, strides, softmax_scale, causal, dtype, workspace, stream);
+}
+
+// ---------------------------------------------- allocation-free forward
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, tight serving loops, harnesses that forbid hipMalloc):
+// scree_attn_fwd_noalloc builds the schedule in this file-scope array
+// instead of a caller's workspace.  Every GPU the library runs on holds its
+// own copy until the process ends.  Host code must not use the array's name
+// as an address (that is a host-side stand-in): each device's address comes
+// from hipGetSymbolAddress, taken once per device with that device current,
+// and only that address is passed to kernels.  The scheduler rewrites the
+// header and every item it publishes on each call, so nothing needs
+// clearing; two calls that overlap on one GPU race on the array.
+static __device__ __align__(256) unsigned char scratch[SCREE_ATTN_NOALLOC_SCHEDULE_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_for_current_device(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(SCREE_ERR_HIP, "%s: no usable current device (%s)", fn, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(SCREE_ERR_HIP, "%s: hipGetSymbolAddress of the static schedule failed: %s",
+                       fn, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SCREE_OK;
+}
+}  // namespace
+
+extern "C" int scree_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
+                                      float* lse, const int32_t* cu_seqlens, int batch,
+                                      int64_t total_tokens, int heads, int kv_heads, int head_dim,
+                                      const int64_t* strides, float softmax_scale, int causal,
+                                      int dtype, void* stream) {
+  const char* fn = "scree_attn_fwd_noalloc";
+  const size_t need = scree_attn_workspace_bytes(batch, total_tokens, head_dim);
+  if (need > (size_t)SCREE_ATTN_NOALLOC_SCHEDULE_BYTES)
+    return set_error(SCREE_ERR_UNSUPPORTED,
+                     "%s: the schedule for batch %d, total_tokens %lld needs %zu bytes, more than "
+                     "the %d-byte static scratch; use scree_attn_fwd with a workspace",
+                     fn, batch, (long long)total_tokens, need, SCREE_ATTN_NOALLOC_SCHEDULE_BYTES);
+  void* ws = nullptr;
+  // validate everything before the first launch (a stand-in size: the
+  // static array is checked against the schedule's need above)
+  int rc = check_fwd(fn, q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, kv_heads,
+                     head_dim, strides, dtype, reinterpret_cast<void*>(1),
+                     SCREE_ATTN_NOALLOC_SCHEDULE_BYTES);
+  if (rc) return rc;
+  if (total_tokens == 0) return SCREE_OK;
+  if ((rc = scratch_for_current_device(fn, &ws))) return rc;
+  rc = scree_attn_schedule(cu_seqlens, batch, total_tokens, head_dim, causal, ws,
+                           SCREE_ATTN_NOALLOC_SCHEDULE_BYTES, stream);
+  if (rc) return rc;
+  return launch_fwd(fn, q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, kv_heads,
+                    head_dim, strides, softmax_scale, causal, dtype, ws, stream);
 }
 
 extern "C" int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,

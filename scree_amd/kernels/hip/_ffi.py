@@ -44,6 +44,7 @@ _SIGNATURES = {
     "scree_attn_bwd_dkv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P, _F, _I, _I, _P,
                                 _S, _P]),
     "scree_attn_fwd_gqa": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F, _I, _I, _P, _S, _P]),
+    "scree_attn_fwd_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F, _I, _I, _P]),
     "scree_attn_bwd_gqa": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F,
                                 _I, _I, _P, _S, _P]),
     "scree_attn_bwd_dq_gqa": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _F, _I,
