@@ -397,11 +397,15 @@ __device__ __forceinline__ void poison_stats(float* __restrict__ p, int total, i
     for (int i = threadIdx.x; i < heads; i += blockDim.x) p[t * heads + i] = __builtin_nanf("");
 }
 
-// A softmax row's reference maximum is raised only when the block maximum
-// exceeds it by more than this many powers of two; p = 2^(s*c - m*c) then
-// stays <= 2^8, which fp32 sums and fp16/bf16 operands hold exactly as well
-// as values <= 1 (same relative precision), and most blocks skip the O rescale.
-constexpr float kRescaleLog2Gap = 8.0f;
+// The forward keeps a reference maximum m per softmax row and forms weights
+// p = 2^(s*c - m*c) without first taking each tile's maximum: a lane checks
+// the sum of its 16 weights of the tile instead.  The weights are >= 0, so a
+// sum <= kSumLimit bounds every weight by 2^8, which fp32 sums and fp16/bf16
+// operands hold with the same relative precision as values <= 1.  Only when
+// some lane's sum exceeds it (or is NaN) does the wave take the tile maximum,
+// raise m, rescale O and the row sum, and form the weights again -- on the
+// first tile of every item (m starts at -1e30) and rarely after.
+constexpr float kSumLimit = 256.0f;
 
 // ------------------------------------------------------- tile staging
 // Direct-to-LDS tiles.  A ROWS x D tile of one head is copied from HBM into
@@ -525,14 +529,14 @@ struct FwdState {
   int koff[D / 16];         // swizzled K row-read offsets
   int2 voffs[D / 32];       // swizzled V transposed-read offsets
   f32x16 oacc[D / 32];      // O^T accumulators
-  float m_run, l_run;       // running max (raw scores) and row sum (this lane's keys)
-  float m_thresh, neg_mb;   // m_run + rescale_gap and -m_run * scale_log2 (change on rescale)
+  float m_run, l_run;       // reference max (raw scores) and row sum (this lane's keys)
+  float neg_mb;             // -m_run * scale_log2
   DmaTile<T, D, kBN> dK, dV;
   const T* kh;
   const T* vh;
   int64_t krow, vrow;
   int L, nkb, kend_wave, qw0, wave, lr, g;
-  float scale_log2, rescale_gap;
+  float scale_log2;
 };
 
 // v_max3_f32 written out: for fmaxf the compiler first canonicalises every
@@ -544,13 +548,91 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
   return r;
 }
 
-// One 64-key block kb: start the DMA of block kb + 1 into `nxt`, then compute
-// on `cur` (K tile, then V tile).  The restrict qualifiers tell the compiler
-// the two buffers are disjoint, so it keeps the DMA in flight across the reads.
+// Sum of a lane's 16 unrounded weights of a tile, in fp32 (two chains).
+__device__ __forceinline__ float tile_sum(const f32x16& p) {
+  float x = p[0], y = p[1];
+#pragma unroll
+  for (int i = 2; i < 16; i += 2) {
+    x += p[i];
+    y += p[i + 1];
+  }
+  return x + y;
+}
+
+// Maximum of a 32-key score tile for this lane's query (both wave halves).
+__device__ __forceinline__ float tile_max(const f32x16& s) {
+  float ma = max3f(s[0], s[1], s[2]);
+  float mc = max3f(s[3], s[4], s[5]);
+  ma = max3f(ma, s[6], s[7]);
+  mc = max3f(mc, s[8], s[9]);
+  ma = max3f(ma, s[10], s[11]);
+  mc = max3f(mc, s[12], s[13]);
+  ma = max3f(ma, s[14], s[15]);
+  float lo, hi;
+  half_pair(max3f(ma, mc, mc), lo, hi);
+  return max3f(lo, hi, hi);
+}
+
+// Mask (to -inf) the keys of the 32-key score tile at tbase that this lane's
+// query may not see: above the diagonal (causal) or past the sequence.
 template <typename T, int D, bool CAUSAL>
+__device__ __forceinline__ void fwd_mask(const FwdState<T, D>& st, f32x16& s, int tbase) {
+  if (CAUSAL) {
+    if (tbase == st.qw0) mask_rows_above(s, st.lr - 4 * st.g);  // the diagonal tile
+  } else if (tbase + 32 > st.L) {
+    mask_rows_above(s, st.L - 1 - tbase - 4 * st.g);
+  }
+}
+
+// Weights p = 2^(s*c - m*c) of a score tile and this lane's fp32 sum of them.
+template <typename T, int D>
+__device__ __forceinline__ float fwd_weights(const FwdState<T, D>& st, const f32x16& s, f32x16& p) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(s[i], st.scale_log2, st.neg_mb));
+  return tile_sum(p);
+}
+
+// The rare path: some lane's weights summed past kSumLimit (or to NaN).
+// Raise the reference maximum to the tile's, rescale O and the row sum, and
+// form the tile's weights again.
+template <typename T, int D>
+__device__ __forceinline__ void fwd_rescale(FwdState<T, D>& st, const f32x16& s, f32x16& p, float& ls) {
+  const float m_new = fmaxf(st.m_run, tile_max(s));
+  const float alpha = fast_exp2((st.m_run - m_new) * st.scale_log2);
+  st.l_run *= alpha;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st.oacc[dt][i] *= alpha;
+  st.m_run = m_new;
+  st.neg_mb = -m_new * st.scale_log2;
+  ls = fwd_weights(st, s, p);
+}
+
+// O^T += V^T P^T for one tile: the weights rounded to T as the B operand,
+// V^T read transposed from the tile's 32 rows at sVt.
+template <typename T, int D>
+__device__ __forceinline__ void fwd_pv(FwdState<T, D>& st, const f32x16& p, const T* sVt) {
+  typedef typename VecT<T>::x8 x8;
+  const x8 pf0 = pack_frag<T>(p, 0), pf1 = pack_frag<T>(p, 8);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) st.oacc[dt] = mfma32(lds_frag_tr(sVt, st.voffs[dt]), pf0, st.oacc[dt]);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+    st.oacc[dt] = mfma32(lds_frag_tr(sVt + 16 * D, st.voffs[dt]), pf1, st.oacc[dt]);
+}
+
+// One 64-key block kb: start the DMA of block kb + 1 into `nxt`, then compute
+// on `cur` (K tile, then V tile).  FULL: every live wave has both 32-key
+// tiles of the block and none needs a mask (blocks before the item's first
+// query, or before a partial last block), so the block runs without the
+// per-tile checks.  Both score tiles are issued before the first tile's
+// softmax, whose VALU work then overlaps the second tile's MFMAs.  The
+// restrict qualifiers tell the compiler the two buffers are disjoint, so it
+// keeps the DMA in flight across the reads.
+template <typename T, int D, bool CAUSAL, bool FULL>
 __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* __restrict__ cur,
                                           T* __restrict__ nxt) {
-  typedef typename VecT<T>::x8 x8;
   constexpr int TILE = kBN * D;
   const T* sK = cur;
   const T* sV = cur + TILE;
@@ -559,70 +641,43 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
     st.dV.load(nxt + TILE, st.vh, st.vrow, (kb + 1) * kBN, st.L, st.wave);
   }
   const int kbase = kb * kBN;
-  const int nt = kbase < st.kend_wave ? (kbase + 32 < st.kend_wave ? 2 : 1) : 0;
-  f32x16 snext;
+  // (waves whose rows all lie past the sequence have kend_wave = 0: no tiles)
+  const int nt = FULL ? (st.kend_wave > 0 ? 2 : 0)
+                      : kbase < st.kend_wave ? (kbase + 32 < st.kend_wave ? 2 : 1) : 0;
   if (nt > 0) {
-    snext = zero16();
+    f32x16 s0 = zero16(), s1, p0, p1;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) snext = mfma32(lds_frag16(sK + st.koff[s]), st.qf[s], snext);
-  }
+    for (int s = 0; s < D / 16; ++s) s0 = mfma32(lds_frag16(sK + st.koff[s]), st.qf[s], s0);
+    if (FULL) {
+      s1 = zero16();
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if (t >= nt) break;
-    f32x16 sacc = snext;
-    if (t + 1 < nt) {  // issue the next tile's scores before this tile's softmax
-      snext = zero16();
+      for (int s = 0; s < D / 16; ++s) s1 = mfma32(lds_frag16(sK + 32 * D + st.koff[s]), st.qf[s], s1);
+      float ls0 = fwd_weights(st, s0, p0);
+      if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+      st.l_run += ls0;
+      fwd_pv(st, p0, sV);
+      float ls1 = fwd_weights(st, s1, p1);
+      if (__any(!(ls1 <= kSumLimit))) fwd_rescale(st, s1, p1, ls1);
+      st.l_run += ls1;
+      fwd_pv(st, p1, sV + 32 * D);
+    } else {
+      if (nt > 1) {
+        s1 = zero16();
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s)
-        snext = mfma32(lds_frag16(sK + 32 * D + st.koff[s]), st.qf[s], snext);
-    }
-    const int tbase = kbase + 32 * t;
-    if (CAUSAL) {
-      if (tbase == st.qw0) mask_rows_above(sacc, st.lr - 4 * st.g);  // the diagonal tile
-    } else if (tbase + 32 > st.L) {
-      mask_rows_above(sacc, st.L - 1 - tbase - 4 * st.g);
-    }
-    // tile max: two interleaved max3 chains, then across the wave's halves
-    float ma = max3f(sacc[0], sacc[1], sacc[2]);
-    float mc = max3f(sacc[3], sacc[4], sacc[5]);
-    ma = max3f(ma, sacc[6], sacc[7]);
-    mc = max3f(mc, sacc[8], sacc[9]);
-    ma = max3f(ma, sacc[10], sacc[11]);
-    mc = max3f(mc, sacc[12], sacc[13]);
-    ma = max3f(ma, sacc[14], sacc[15]);
-    float lo, hi;
-    half_pair(max3f(ma, mc, mc), lo, hi);
-    const float mx = max3f(lo, hi, hi);
-    const bool grow = mx > st.m_thresh;
-    if (__any(grow)) {
-      const float m_new = grow ? mx : st.m_run;
-      const float alpha = fast_exp2((st.m_run - m_new) * st.scale_log2);
-      st.l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st.oacc[dt][i] *= alpha;
-      st.m_run = m_new;
-      st.m_thresh = m_new + st.rescale_gap;
-      st.neg_mb = -m_new * st.scale_log2;
-    }
-    // the row sum in fp32, of the unrounded weights (two partial chains)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sacc[i] = fast_exp2(fmaf(sacc[i], st.scale_log2, st.neg_mb));
-    float ls0 = st.l_run + sacc[0], ls1 = sacc[1];
-#pragma unroll
-    for (int i = 2; i < 16; i += 2) {
-      ls0 += sacc[i];
-      ls1 += sacc[i + 1];
-    }
-    st.l_run = ls0 + ls1;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const x8 pf = pack_frag<T>(sacc, 8 * hh);
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-        st.oacc[dt] = mfma32(lds_frag_tr(sV + (32 * t + 16 * hh) * D, st.voffs[dt]), pf,
-                             st.oacc[dt]);
+        for (int s = 0; s < D / 16; ++s) s1 = mfma32(lds_frag16(sK + 32 * D + st.koff[s]), st.qf[s], s1);
+      }
+      fwd_mask<T, D, CAUSAL>(st, s0, kbase);
+      float ls0 = fwd_weights(st, s0, p0);
+      if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+      st.l_run += ls0;
+      fwd_pv(st, p0, sV);
+      if (nt > 1) {
+        fwd_mask<T, D, CAUSAL>(st, s1, kbase + 32);
+        float ls1 = fwd_weights(st, s1, p1);
+        if (__any(!(ls1 <= kSumLimit))) fwd_rescale(st, s1, p1, ls1);
+        st.l_run += ls1;
+        fwd_pv(st, p1, sV + 32 * D);
+      }
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block kb + 1 has landed
@@ -689,20 +744,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) st.voffs[dt] = swz_tr_off<D>(st.lr, st.g, dt);
   st.scale_log2 = scale_log2;
-  st.rescale_gap = kRescaleLog2Gap / scale_log2;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) st.oacc[dt] = zero16();
   st.m_run = kMaxInit;
   st.l_run = 0.f;
-  st.m_thresh = kMaxInit + st.rescale_gap;
   st.neg_mb = -kMaxInit * scale_log2;
 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // Blocks [0, nfull) need no mask and give every wave two tiles: those
+  // before the item's first query (causal) or before a partial last block.
   // Unrolled by two so that each call sees its buffers at fixed positions.
-  for (int kb = 0; kb < st.nkb; kb += 2) {
-    fwd_block<T, D, CAUSAL>(st, kb, bufA, bufB);
-    if (kb + 1 < st.nkb) fwd_block<T, D, CAUSAL>(st, kb + 1, bufB, bufA);
+  const int nfull = CAUSAL ? min(q0, L) / kBN : L / kBN;
+  int kb = 0;
+  for (; kb + 1 < nfull; kb += 2) {
+    fwd_block<T, D, CAUSAL, true>(st, kb, bufA, bufB);
+    fwd_block<T, D, CAUSAL, true>(st, kb + 1, bufB, bufA);
+  }
+  if (kb < nfull) {  // odd count: the last full block, then swap the buffers
+    fwd_block<T, D, CAUSAL, true>(st, kb, bufA, bufB);
+    T* t = bufA;
+    bufA = bufB;
+    bufB = t;
+    ++kb;
+  }
+  for (; kb < st.nkb; kb += 2) {
+    fwd_block<T, D, CAUSAL, false>(st, kb, bufA, bufB);
+    if (kb + 1 < st.nkb) fwd_block<T, D, CAUSAL, false>(st, kb + 1, bufB, bufA);
   }
   if (wave_live) {  // the last block's barrier freed the tile buffers: stage O there
     const float l_tot = halves_sum(st.l_run);

@@ -218,6 +218,7 @@ def test_config5_sampled_heads_bf16():
 
 @pytest.mark.parametrize("causal", [True, False])
 def test_schedule_bit_exact(causal):
+    from scree_amd.kernels.hip import attention as A
     from scree_amd.kernels.hip import attention_schedule, schedule_items
 
     cases = [EDGE_LENGTHS, [5], [0, 0, 3], workloads.config3().lengths,
@@ -225,11 +226,16 @@ def test_schedule_bit_exact(causal):
     for lengths in cases:
         say(f"case: schedule B={len(lengths)} N={sum(lengths)} causal={causal}")
         off, cu = cu_of(lengths)
-        ws = attention_schedule(cu, int(sum(lengths)), 64, causal)
+        n = int(sum(lengths))
+        ws = torch.full((A.workspace_bytes(len(lengths), n, 64),), 255, dtype=torch.uint8,
+                        device="cuda")  # stale bytes: the scheduler must rewrite what it uses
+        attention_schedule(cu, n, 64, causal, ws)
         count, items = schedule_items(ws)
         want = build_schedule(off, 128, causal)
         assert count == len(want)
         np.testing.assert_array_equal(items.numpy(), want)
+        header = ws[:16].view(torch.int32).cpu().tolist()
+        assert header == [len(want), len(lengths), 128, int(causal)]
 
 
 def test_strided_qkv_views_match_contiguous():
