@@ -155,12 +155,12 @@ int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, flo
  * results as scree_attn_fwd_gqa minus the workspace: the schedule is built
  * on `stream` (as scree_attn_schedule would) into a static device array of
  * SCREE_ATTN_NOALLOC_SCHEDULE_BYTES per GPU, which holds
- * scree_attn_workspace_bytes() up to that size: (ceil(total_tokens / 128) +
- * batch) * 16 + 16 bytes, i.e. about 8 million tokens.  Larger problems get
+ * scree_attn_workspace_bytes() up to that size: 2 * (ceil(total_tokens / 128)
+ * + batch) * 16 + 16 bytes, i.e. about 8 million tokens.  Larger problems get
  * SCREE_ERR_UNSUPPORTED before anything is launched.  Calls no allocating
  * routine.  Calls that overlap on one GPU (several streams or host threads)
  * race on the array; serialise them. */
-#define SCREE_ATTN_NOALLOC_SCHEDULE_BYTES (1 << 20)
+#define SCREE_ATTN_NOALLOC_SCHEDULE_BYTES (1 << 21)
 int scree_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o, float* lse,
                            const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
                            int kv_heads, int head_dim, const int64_t* strides,

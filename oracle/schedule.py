@@ -19,6 +19,11 @@ first:
 
 The key-block-major list used by the dK/dV pass is the same list with
 ``blk -> nblk - 1 - blk``, whose work ``nblk - blk`` then matches ``c``.
+
+A second list holds the same items sequence by sequence (``build_schedule_by_sequence``):
+sequences in rank order, each with its blocks from the last down.  Launches
+that give each XCD one head at a time read it, so that the resident
+workgroups of an XCD share one sequence's K/V.
 """
 
 from __future__ import annotations
@@ -66,3 +71,12 @@ def build_schedule(offsets, block: int, causal: bool, max_class: int = 4096) -> 
 def item_cost(item, nblk, causal: bool) -> int:
     s, b = int(item[0]), int(item[1])
     return b + 1 if causal else int(nblk[s])
+
+
+def build_schedule_by_sequence(offsets, block: int) -> np.ndarray:
+    """The sequence-major list: ``(seq, blk)`` for sequences in ``(-nblk, seq)``
+    rank order, each sequence's blocks ``nblk - 1`` down to ``0``."""
+    nblk = block_counts(offsets, block)
+    items = [(s, b) for s in seq_order(nblk) for b in range(int(nblk[s]) - 1, -1, -1)]
+    return np.asarray(items, dtype=np.int32).reshape(-1, 2)
+

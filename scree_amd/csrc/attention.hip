@@ -44,8 +44,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
 
 // ------------------------------------------------------------ workspace
-// int32 header[4] = {item count T, batch, kBM, causal}, then int4 items[Tmax]
-// = {seq, blk, start, len}.  start/len are the sequence's offsets clamped to
+// int32 header[4] = {item count T, batch, kBM, causal}, then two lists of
+// int4 items[Tmax] = {seq, blk, start, len}: longest-work-first, then the same
+// items sequence by sequence (attn_schedule_kernel).  start/len are the sequence's offsets clamped to
 // [0, total_tokens], so attention kernels never index outside the tensors
 // even for malformed offsets; if those would make T exceed Tmax the
 // scheduler publishes T = 0 (no work) and header[1] = -1, and the attention
@@ -53,6 +54,7 @@ constexpr float kNegInf = -__builtin_inff();
 constexpr size_t kHeaderBytes = 16;
 
 inline int64_t tmax_for(int batch, int64_t total) { return (total + kBM - 1) / kBM + batch; }
+inline size_t schedule_bytes(int64_t tmax) { return kHeaderBytes + 2 * (size_t)tmax * sizeof(int4); }
 
 // ------------------------------------------------------------ scheduler
 __device__ int wave_incl_scan(int v) {
@@ -65,33 +67,47 @@ __device__ int wave_incl_scan(int v) {
   return v;
 }
 
-// In-place exclusive scan of a[0..n) held in LDS by the whole block; returns
-// the total.  Caller synchronises before; this synchronises after.
-__device__ int block_excl_scan(int* a, int n, int* wtot) {
+// In-place exclusive scans of a[0..n) and b[0..n), held in LDS by the whole
+// block, sharing their barriers; the totals go to ta / tb.  wtot holds 64
+// ints.  Caller synchronises before; this synchronises after.
+__device__ void block_excl_scan2(int* a, int* b, int n, int* wtot, int& ta, int& tb) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int lane = tid & (kWave - 1), wave = tid / kWave, nw = nt / kWave;
   const int per = (n + nt - 1) / nt;
   const int beg = min(n, tid * per), end = min(n, beg + per);
-  int local = 0;
-  for (int i = beg; i < end; ++i) local += a[i];
-  const int incl = wave_incl_scan(local);
-  if (lane == kWave - 1) wtot[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    int t = lane < nw ? wtot[lane] : 0;
-    t = wave_incl_scan(t);
-    if (lane < nw) wtot[16 + lane] = t;  // inclusive prefix of wave totals
-  }
-  __syncthreads();
-  int run = incl - local + (wave > 0 ? wtot[16 + wave - 1] : 0);
+  int la = 0, lb = 0;
   for (int i = beg; i < end; ++i) {
-    const int t = a[i];
-    a[i] = run;
-    run += t;
+    la += a[i];
+    lb += b[i];
   }
-  const int total = wtot[16 + nw - 1];
+  const int ia = wave_incl_scan(la), ib = wave_incl_scan(lb);
+  if (lane == kWave - 1) {
+    wtot[wave] = ia;
+    wtot[32 + wave] = ib;
+  }
   __syncthreads();
-  return total;
+  if (wave == 0) {  // inclusive prefixes of the wave totals
+    int t = lane < nw ? wtot[lane] : 0, u = lane < nw ? wtot[32 + lane] : 0;
+    t = wave_incl_scan(t);
+    u = wave_incl_scan(u);
+    if (lane < nw) {
+      wtot[16 + lane] = t;
+      wtot[48 + lane] = u;
+    }
+  }
+  __syncthreads();
+  int ra = ia - la + (wave > 0 ? wtot[16 + wave - 1] : 0);
+  int rb = ib - lb + (wave > 0 ? wtot[48 + wave - 1] : 0);
+  for (int i = beg; i < end; ++i) {
+    const int t = a[i], u = b[i];
+    a[i] = ra;
+    b[i] = rb;
+    ra += t;
+    rb += u;
+  }
+  ta = wtot[16 + nw - 1];
+  tb = wtot[48 + nw - 1];
+  __syncthreads();
 }
 
 // One 1024-thread block.  See oracle/schedule.py for the order produced.
@@ -107,7 +123,7 @@ __global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __re
   __shared__ int s_sorted_scan[kMaxBatch + 1];
   __shared__ int s_nat_scan[kMaxBatch + 1];
   __shared__ int s_cls[kMaxClass + 2];
-  __shared__ int s_wtot[32];
+  __shared__ int s_wtot[64];
   __shared__ int s_cmax;
   const int tid = threadIdx.x, nt = blockDim.x;
   if (tid == 0) s_cmax = 0;
@@ -137,12 +153,15 @@ __global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __re
     s_sorted_scan[r] = mine;
   }
   __syncthreads();
-  const int total = block_excl_scan(s_nat_scan, batch, s_wtot);  // natural-order item index base
+  // Item bases of each sequence: in natural order (s_nat_scan), and in rank
+  // order (s_sorted_scan), how the non-causal and the sequence-major lists
+  // place sequences.
+  int total, total_ranked;
+  block_excl_scan2(s_nat_scan, s_sorted_scan, batch, s_wtot, total, total_ranked);
+  (void)total_ranked;  // equals total
   if (tid == 0) s_nat_scan[batch] = total;
   const bool by_class = causal && cmax <= kMaxClass;
-  if (!causal) {
-    block_excl_scan(s_sorted_scan, batch, s_wtot);
-  } else if (by_class) {
+  if (by_class) {
     // Histogram of nblk, then two suffix passes by one wave:
     // A(c) = #{s : nblk_s >= c} and offs(c) = sum_{c' > c} A(c').
     for (int c = tid; c <= cmax + 1; c += nt) s_cls[c] = 0;
@@ -195,7 +214,10 @@ __global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __re
     if (!causal) p = s_sorted_scan[s_rank[s]] + b;
     else if (by_class) p = s_cls[b + 1] + s_rank[s];
     else p = i;
-    items[p] = make_int4(s, b, s_start[s], s_len[s]);
+    const int4 it = make_int4(s, b, s_start[s], s_len[s]);
+    items[p] = it;
+    // sequence-major: sequences in rank order, each one's blocks from the last
+    items[tmax + s_sorted_scan[s_rank[s]] + s_nblk[s] - 1 - b] = it;
   }
   if (tid == 0) {
     header[0] = fits ? total : 0;
@@ -1046,6 +1068,7 @@ struct DkvState {
   const float* delta_h;
   int64_t qrow, drow;
   int heads, L, qbeg, nqb, kw0, wave, lr, g;
+  int qfirst, qstep;              // query row of block 0 and the step between blocks (+-BQ)
   bool wave_live;
   float pl, pd;                   // staged LSE and Delta of one query row
   float scale_log2;
@@ -1076,10 +1099,10 @@ __device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __
   constexpr int TILE = BQ * D;
   const T* sQ = cur;
   const T* sO = cur + TILE;
-  const int qb = st.qbeg + b * BQ;
+  const int qb = st.qfirst + b * st.qstep;
   if (b + 1 < st.nqb) {
-    st.dQ.load(nxt, st.qh, st.qrow, qb + BQ, st.L, st.wave);
-    st.dO.load(nxt + TILE, st.dh, st.drow, qb + BQ, st.L, st.wave);
+    st.dQ.load(nxt, st.qh, st.qrow, qb + st.qstep, st.L, st.wave);
+    st.dO.load(nxt + TILE, st.dh, st.drow, qb + st.qstep, st.L, st.wave);
   }
   if (st.wave_live) {
 #pragma unroll
@@ -1154,7 +1177,7 @@ __device__ __forceinline__ void dkv_step(DkvState<T, D>& st, int b, const T* cur
                                          const float* lcur, float* lnxt, const T* kl) {
   constexpr int BQ = DkvState<T, D>::BQ;
   const bool more = b + 1 < st.nqb;
-  if (more && threadIdx.x < BQ) dkv_load_rows(st, st.qbeg + (b + 1) * BQ + (int)threadIdx.x);
+  if (more && threadIdx.x < BQ) dkv_load_rows(st, st.qfirst + (b + 1) * st.qstep + (int)threadIdx.x);
   dkv_block<T, D, CAUSAL>(st, b, cur, nxt, lcur, kl);
   if (more && threadIdx.x < BQ) dkv_store_rows(lnxt, BQ, st.pl, st.pd);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's share of block b + 1 has landed
@@ -1228,7 +1251,7 @@ constexpr int dkv_waves() {
   return D <= 32 || (D == 64 && CAUSAL) ? 3 : 2;
 }
 
-template <typename T, int D, bool CAUSAL, bool SPLIT>
+template <typename T, int D, bool CAUSAL, bool SPLIT, bool REV>
 __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_dkv_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -1283,6 +1306,11 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   st.qbeg = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
   st.nqb = (L - st.qbeg + BQ - 1) / BQ;
   st.scale_log2 = scale_log2;
+  // REV (head-major launches, sequence-major list): sweep the query blocks
+  // from the last down, so the resident items of one sequence all start
+  // there and move together; upward sweeps start at their own key blocks.
+  st.qstep = REV ? -BQ : BQ;
+  st.qfirst = REV ? st.qbeg + (st.nqb - 1) * BQ : st.qbeg;
 
   T* bufA = smem;
   T* bufB = smem + BUF;
@@ -1294,10 +1322,10 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
     st.dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
     st.lse_h = lse + (int64_t)start * heads + h;
     st.delta_h = delta + (int64_t)start * heads + h;
-    st.dQ.load(bufA, st.qh, sq.row, st.qbeg, L, st.wave);
-    st.dO.load(bufA + TILE, st.dh, sdo.row, st.qbeg, L, st.wave);
+    st.dQ.load(bufA, st.qh, sq.row, st.qfirst, L, st.wave);
+    st.dO.load(bufA + TILE, st.dh, sdo.row, st.qfirst, L, st.wave);
     if (threadIdx.x < BQ) {
-      dkv_load_rows(st, st.qbeg + (int)threadIdx.x);
+      dkv_load_rows(st, st.qfirst + (int)threadIdx.x);
       dkv_store_rows(sLD0, BQ, st.pl, st.pd);
     }
   };
@@ -1443,6 +1471,15 @@ inline size_t dkv_split_bytes(int64_t tmax, int kv_heads, int gsplit, int head_d
 inline int attn_head_major(int heads, int tmax) {
   return (heads % kXcds == 0) && ((int64_t)tmax * heads / kXcds >= 512) ? 1 : 0;
 }
+// The item list a launch reads.  Head-major launches take the sequence-major
+// list: an XCD's resident workgroups then hold row blocks of one sequence and
+// head, which read the same K/V prefix (or, in the dK/dV pass, the same Q /
+// dO suffix) at about the same time, so the XCD's L2 serves most of the
+// re-reads; in longest-work-first order they mix sequences and drift apart.
+inline const int4* schedule_list(const void* ws, int tmax, int head_major) {
+  return reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes) +
+         (head_major ? tmax : 0);
+}
 
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
@@ -1451,10 +1488,11 @@ void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* l
                   hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
-  const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
+  const int hm = attn_head_major(heads, tmax);
+  const int4* items = schedule_list(ws, tmax, hm);
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(o), lse, header, items, tmax, attn_head_major(heads, tmax),
+                     static_cast<T*>(o), lse, header, items, tmax, hm,
                      heads, heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
                      Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e, total);
 }
@@ -1467,12 +1505,13 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
                      int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int32_t* header = static_cast<const int32_t*>(ws);
-  const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
+  const int hm = attn_head_major(heads, tmax);
+  const int4* items = schedule_list(ws, tmax, hm);
   hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<const T*>(o), lse, delta, static_cast<T*>(dq), header, items,
-                     tmax, attn_head_major(heads, tmax), heads, heads / kv_heads,
+                     tmax, hm, heads, heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
                      scale * kLog2e, total);
@@ -1487,15 +1526,19 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
   // one workgroup per (item, K/V head, part of the head group)
   const int64_t grid = (int64_t)tmax * kv_heads * gsplit;
   const int32_t* header = static_cast<const int32_t*>(ws);
-  const int4* items = reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes);
+  const int hm = attn_head_major(kv_heads * gsplit, tmax);
+  const int4* items = schedule_list(ws, tmax, hm);
   // the split epilogue has a kernel of its own: its registers would cost the
   // unsplit kernel a wave per SIMD at D = 64
-  auto kern = gsplit > 1 ? attn_bwd_dkv_kernel<T, D, C, true> : attn_bwd_dkv_kernel<T, D, C, false>;
+  // (a split group never has the many rounds of a head-major launch)
+  auto kern = gsplit > 1 ? attn_bwd_dkv_kernel<T, D, C, true, false>
+              : hm       ? attn_bwd_dkv_kernel<T, D, C, false, true>
+                         : attn_bwd_dkv_kernel<T, D, C, false, false>;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), lse, delta,
-                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, tmax,
-                     attn_head_major(kv_heads * gsplit, tmax), kv_heads, heads / kv_heads,
+                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, tmax, hm, kv_heads,
+                     heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
                      scale * kLog2e, gsplit, partial, total);
@@ -1527,7 +1570,7 @@ using namespace scree;
 extern "C" size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim) {
   (void)head_dim;
   if (batch < 1 || total_tokens < 0) return 0;
-  return kHeaderBytes + (size_t)tmax_for(batch, total_tokens) * sizeof(int4);
+  return schedule_bytes(tmax_for(batch, total_tokens));
 }
 
 extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_tokens,

@@ -113,15 +113,19 @@ def attention_schedule(cu_seqlens: torch.Tensor, total_tokens: int, head_dim: in
     return workspace
 
 
-def schedule_items(workspace: torch.Tensor, with_ranges: bool = False):
+def schedule_items(workspace: torch.Tensor, with_ranges: bool = False, by_sequence: bool = False,
+                   tmax: int = 0):
     """Decode a schedule workspace into ``(count, items)`` on the host (tests).
 
     ``items`` is ``(count, 2)`` of ``(seq, blk)``, or ``(count, 4)`` with the
-    sequence's clamped ``(start, len)`` when ``with_ranges``.
+    sequence's clamped ``(start, len)`` when ``with_ranges``.  The workspace
+    holds two lists of ``tmax = ceil(total / 128) + batch`` slots: longest work
+    first, then (``by_sequence``) the same items sequence by sequence.
     """
     header = workspace[:16].view(torch.int32).cpu()
     count = int(header[0])
-    items = workspace[16:16 + 16 * count].view(torch.int32).reshape(-1, 4).cpu()
+    base = 16 + (16 * tmax if by_sequence else 0)
+    items = workspace[base:base + 16 * count].view(torch.int32).reshape(-1, 4).cpu()
     return count, (items if with_ranges else items[:, :2].contiguous())
 
 

@@ -69,8 +69,8 @@ def test_attention_validation_errors():
 
 def test_workspace_sizes():
     lib = _ffi.lib()
-    # header + (ceil(N/128) + B) int4 items
-    assert lib.scree_attn_workspace_bytes(16, 12160, 64) == 16 + 16 * (95 + 16)
+    # header + two lists of (ceil(N/128) + B) int4 items
+    assert lib.scree_attn_workspace_bytes(16, 12160, 64) == 16 + 2 * 16 * (95 + 16)
     assert lib.scree_attn_workspace_bytes(0, 10, 64) == 0
     assert lib.scree_norm_bwd_workspace_bytes(19758, 4096) == 512 * 2 * 4096 * 4
     assert lib.scree_norm_bwd_workspace_bytes(10, 100) == 2 * 2 * 100 * 4

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle.attention import attention_bwd, attention_fwd
-from oracle.schedule import build_schedule
+from oracle.schedule import build_schedule, build_schedule_by_sequence
 from parity import UNIT, attn_abs_terms, check_close, cu_of, np64, randn, say
 from scree_amd import workloads
 
@@ -216,6 +216,43 @@ def test_config5_sampled_heads_bf16():
         del sl
 
 
+def test_head_major_launch_fp16_d64_both_masks():
+    """A grid of many rounds per XCD (config 5's lengths, 8 heads of 64:
+    689 items x 8 heads) takes the head-major launch, the sequence-major item
+    list and the downward query sweep of dK/dV.  Checked on two heads of
+    three sequences, causal and not."""
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
+
+    c = workloads.config5()
+    n, h, d = c.total, 8, 64
+    off, cu = cu_of(c.lengths)
+    q, k, v, do = (randn((n, h, d), torch.float16, 80 + s) for s in range(4))
+    order = np.argsort(c.lengths)
+    picks = sorted({int(order[0]), int(order[len(order) // 2]), int(order[-6])})
+    heads = [1, 6]
+    u = UNIT[torch.float16]
+    for causal in (True, False):
+        say(f"case: head-major N={n} H={h} D={d} fp16 causal={causal}")
+        out, lse = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True)
+        dq, dk, dv = varlen_attention_hip_backward(do, q, k, v, out, lse, cu, causal=causal)
+        torch.cuda.synchronize()
+        for s in picks:
+            a, b = int(off[s]), int(off[s + 1])
+            say(f"  seq {s} len {b - a} heads {heads}")
+            sub = lambda t: np64(t[a:b][:, heads])  # noqa: E731
+            q64, k64, v64, do64 = sub(q), sub(k), sub(v), sub(do)
+            loff = np.array([0, b - a], dtype=np.int32)
+            ro, rl = attention_fwd(q64, k64, v64, loff, causal=causal, dtype=np.float64)
+            terms = attn_abs_terms(q64, k64, v64, do64, rl, loff, causal)
+            check_close("O", sub(out), ro, 2e-3, extra=2 * terms[0] + np.abs(ro), unit=u)
+            check_close("LSE", lse[a:b][:, heads].cpu().numpy().astype(np.float64), rl,
+                        1e-4 + 1e-5 * np.abs(rl).max())
+            rdq, rdk, rdv, _ = attention_bwd(do64, q64, k64, v64, sub(out), rl, loff, causal=causal)
+            check_close("dQ", sub(dq), rdq, 5e-3, extra=2 * terms[2] + np.abs(rdq), unit=u)
+            check_close("dK", sub(dk), rdk, 5e-3, extra=2 * terms[3] + np.abs(rdk), unit=u)
+            check_close("dV", sub(dv), rdv, 5e-3, extra=2 * terms[1] + np.abs(rdv), unit=u)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_schedule_bit_exact(causal):
     from scree_amd.kernels.hip import attention as A
@@ -236,6 +273,10 @@ def test_schedule_bit_exact(causal):
         np.testing.assert_array_equal(items.numpy(), want)
         header = ws[:16].view(torch.int32).cpu().tolist()
         assert header == [len(want), len(lengths), 128, int(causal)]
+        tmax = (n + 127) // 128 + len(lengths)
+        count2, items2 = schedule_items(ws, by_sequence=True, tmax=tmax)
+        assert count2 == count
+        np.testing.assert_array_equal(items2.numpy(), build_schedule_by_sequence(off, 128))
 
 
 def test_strided_qkv_views_match_contiguous():

@@ -44,3 +44,25 @@ def test_schedule_small_causal_example_by_hand():
     assert items.tolist() == [[0, 2], [0, 1], [2, 1], [0, 0], [2, 0], [1, 0]]
     items = build_schedule(offsets_from_lengths([300, 100, 200]), 128, False)
     assert items.tolist() == [[0, 0], [0, 1], [0, 2], [2, 0], [2, 1], [1, 0]]
+
+
+def test_sequence_major_list_by_hand_and_coverage():
+    from oracle.schedule import build_schedule_by_sequence
+
+    # lengths 300, 100, 200 -> nblk 3, 1, 2; rank: seq0, seq2, seq1
+    items = build_schedule_by_sequence(offsets_from_lengths([300, 100, 200]), 128)
+    assert items.tolist() == [[0, 2], [0, 1], [0, 0], [2, 1], [2, 0], [1, 0]]
+    for lengths in _cases():
+        off = offsets_from_lengths(lengths)
+        a = build_schedule_by_sequence(off, 128)
+        b = build_schedule(off, 128, True)
+        assert sorted(map(tuple, a.tolist())) == sorted(map(tuple, b.tolist()))
+        # each sequence's blocks are contiguous and descending
+        seqs = a[:, 0].tolist()
+        for s in set(seqs):
+            idx = [i for i, x in enumerate(seqs) if x == s]
+            assert idx == list(range(idx[0], idx[0] + len(idx)))
+        for i in range(1, len(a)):
+            if a[i, 0] == a[i - 1, 0]:
+                assert a[i, 1] == a[i - 1, 1] - 1
+

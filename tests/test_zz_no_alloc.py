@@ -16,7 +16,7 @@ from scree_amd import workloads
 from scree_amd.kernels.hip import _ffi
 from scree_amd.kernels.hip import attention as A
 
-LIMIT = 1 << 20  # SCREE_ATTN_NOALLOC_SCHEDULE_BYTES
+LIMIT = 1 << 21  # SCREE_ATTN_NOALLOC_SCHEDULE_BYTES
 
 
 def _strides(*ts):
@@ -62,14 +62,16 @@ def _with_workspace(cu, q, k, v, causal):
 def test_limit_is_rejected_before_any_launch():
     lib = _ffi.lib()
     null = ctypes.c_void_p(0)
-    # 2^27 tokens need (2^20 + 1) * 16 + 16 bytes of schedule: over the limit
+    # 2^27 tokens need 2 * (2^20 + 1) * 16 + 16 bytes of schedule: over the limit
     rc = lib.scree_attn_fwd_noalloc(null, null, null, null, null, null, 1, 1 << 27, 1, 1, 64,
                                     null, 0.125, 1, _ffi.DTYPE_F16, null)
     assert rc == _ffi.SCREE_ERR_UNSUPPORTED
     assert "static scratch" in lib.scree_last_error().decode()
     assert lib.scree_attn_workspace_bytes(1, 1 << 27, 64) > LIMIT
-    # the largest accepted problem fits exactly
-    assert lib.scree_attn_workspace_bytes(1, (LIMIT // 16 - 2) * 128, 64) <= LIMIT
+    # the largest accepted problem fits exactly: two lists of tmax slots
+    tmax = (LIMIT - 16) // 32
+    assert lib.scree_attn_workspace_bytes(1, (tmax - 1) * 128, 64) <= LIMIT
+    assert lib.scree_attn_workspace_bytes(1, tmax * 128, 64) > LIMIT
 
 
 @pytest.mark.gpu
