@@ -31,27 +31,48 @@ constexpr int kMaxChunks = 16;     // 16-byte vectors per lane on the fast path
 // ------------------------------------------------------------------ forward
 // RES (RMSNorm only): the normalised row is h = x + res, rounded to T as a
 // separate addition would round it; h is written out and normalised.
+template <int WAVES>
+constexpr int fwd_threads() { return WAVES * kWave; }
+// LayerNorm's workgroups are kLnWaves rows (waves) that stage the weight and
+// bias rows in LDS once; RMSNorm's are kFwdWaves rows with the weights in
+// registers.
+constexpr int kLnWaves = 8;
+template <bool LAYER>
+constexpr int fwd_waves() { return LAYER ? kLnWaves : kFwdWaves; }
+
 template <typename T, int CHUNKS, bool LAYER, bool RES>
-__global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
+__global__ __launch_bounds__(fwd_threads<fwd_waves<LAYER>()>()) void norm_fwd_vec(
     const T* __restrict__ x, const T* __restrict__ res, const T* __restrict__ w,
     const T* __restrict__ b, T* __restrict__ hout, T* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows, int dim, float eps) {
   constexpr int VEC = 16 / sizeof(T);
+  constexpr int WAVES = fwd_waves<LAYER>();
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x / kWave);
-  if (row >= rows) return;
+  const int64_t row = (int64_t)blockIdx.x * WAVES + (threadIdx.x / kWave);
+  const bool live = row < rows;
   const int nvec = dim / VEC;
   const T* xr = x + row * (int64_t)dim;
   uint4 v[CHUNKS];
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int vi = c * kWave + lane;
-    v[c] = vi < nvec ? ld16_nt(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+    v[c] = live && vi < nvec ? ld16_nt(xr + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
   }
+  // LayerNorm: the block copies the weight and bias rows into LDS while its
+  // rows load (one L2 read per block instead of per row, and off the
+  // registers); the output reads them from there.
+  constexpr int NMAX = LAYER ? CHUNKS * kWave * VEC : 1;
+  __shared__ __align__(16) T wb[2 * NMAX];
+  if constexpr (LAYER) {
+    for (int vi = threadIdx.x; vi < nvec; vi += WAVES * kWave) {
+      *reinterpret_cast<uint4*>(wb + vi * VEC) = w ? ld16(w + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(wb + NMAX + vi * VEC) = b ? ld16(b + (int64_t)vi * VEC) : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  if (!live) return;
   // RMSNorm loads its weight vectors with the row, so their (L2) latency
-  // overlaps the row's instead of following the reduction; LayerNorm, with
-  // the bias too, would lose a wave per SIMD to the registers and keeps the
-  // loads at the output.
+  // overlaps the row's instead of following the reduction.
   constexpr bool kEarlyW = !LAYER;
   uint4 wvs[kEarlyW ? CHUNKS : 1];
   if constexpr (kEarlyW) {
@@ -115,11 +136,12 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_vec(
     const int vi = c * kWave + lane;
     if (vi < nvec) {
       uint4 wv = make_uint4(0, 0, 0, 0), bv = make_uint4(0, 0, 0, 0);
-      if constexpr (kEarlyW)
+      if constexpr (kEarlyW) {
         wv = wvs[c];
-      else if (w)
-        wv = ld16(w + (int64_t)vi * VEC);
-      if (LAYER && b) bv = ld16(b + (int64_t)vi * VEC);
+      } else {
+        wv = *reinterpret_cast<const uint4*>(wb + vi * VEC);
+        bv = *reinterpret_cast<const uint4*>(wb + NMAX + vi * VEC);
+      }
       float f[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
@@ -574,10 +596,12 @@ void launch_fwd_k(const T* xp, const T* rp, const T* wp, const T* bp, T* hp, T* 
   const dim3 block(kFwdWaves * kWave);
   const int d = (int)dim;
   if (fast_path_ok<T>(dim, {xp, rp, wp, bp, hp, yp})) {
+    constexpr int W = fwd_waves<LAYER>();
+    const dim3 vgrid((unsigned)((rows + W - 1) / W)), vblock(W * kWave);
     const int chunks = chunks_for((int)(dim / (16 / sizeof(T))));
 #define SCREE_FWD_CASE(C)                                                                      \
   case C:                                                                                      \
-    hipLaunchKernelGGL((norm_fwd_vec<T, C, LAYER, RES>), grid, block, 0, stream, xp, rp, wp, bp, \
+    hipLaunchKernelGGL((norm_fwd_vec<T, C, LAYER, RES>), vgrid, vblock, 0, stream, xp, rp, wp, bp, \
                        hp, yp, mean, rstd, rows, d, eps);                                      \
     break;
     switch (chunks) {
