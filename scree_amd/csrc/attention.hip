@@ -28,6 +28,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -805,6 +806,31 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   }
 }
 
+// ------------------------------------------- dQ pass: folded score scale
+// The dQ pass needs P = 2^(s * scale*log2(e) - LSE*log2(e)) per score.  In
+// fp16 the factor c = scale*log2(e) is folded into the Q rows it holds in
+// registers (each element multiplied by c in fp32 and rounded once to fp16),
+// and the score accumulator starts at -LSE*log2(e) of the lane's query
+// instead of 0, so the MFMA chain yields the exponent itself and the
+// per-score FMA (16 per 32x32 tile) is gone.  The extra rounding moves an
+// exponent by about 2^-11 * c * sqrt(sum (q_d k_d)^2), a relative error in P
+// below the one fp16 already gives P as an MFMA operand; dQ sums it over one
+// head's keys.  The dK/dV pass keeps the fp32 FMA: its sums run over every
+// query of a head group (8 heads of grouped-query attention), where the
+// same perturbation measured dV 6.9e-3 against the 5e-3 bound.  bf16 (8
+// significant bits) keeps the FMA in both passes.
+template <typename T>
+constexpr bool dq_prescale() {
+  return std::is_same<T, f16>::value;
+}
+template <typename T>
+__device__ __forceinline__ typename VecT<T>::x8 scale_frag(typename VecT<T>::x8 f, float c) {
+  typename VecT<T>::x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = from_f32<T>((float)f[j] * c);
+  return r;
+}
+
 // -------------------------------------------------- backward: dQ and Delta
 // Per item: 128 queries (32 per wave) loop over 64-key blocks.
 //   S^T = K Q^T, dP^T = V dO^T (Q, dO operands in registers; K, V from LDS)
@@ -822,6 +848,7 @@ struct DqState {
   int2 ktr[D / 32];           // swizzled transposed-read offsets (K^T)
   f32x16 dqacc[D / 32];       // dQ^T accumulators
   f32x16 neg_delta;           // dP^T accumulates onto -Delta: it comes out as dP^T - Delta
+  f32x16 neg_lse;             // fp16: S^T accumulates onto -LSE*log2(e) (Q rows pre-scaled)
   float lse2;                 // this lane's LSE * log2(e)
   DmaTile<T, D, kBN> dK, dV;
   const T* kh;
@@ -855,10 +882,11 @@ __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __r
   }
   const int kbase = kb * kBN;
   const int nt = kbase < st.kend_wave ? (kbase + 32 < st.kend_wave ? 2 : 1) : 0;
+  constexpr bool PRE = dq_prescale<T>();
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     if (t >= nt) break;
-    f32x16 sacc = zero16(), pacc = st.neg_delta;
+    f32x16 sacc = PRE ? st.neg_lse : zero16(), pacc = st.neg_delta;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
       sacc = mfma32(lds_frag16(sK + 32 * t * D + st.koff[s]), st.qf[s], sacc);
@@ -867,7 +895,7 @@ __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __r
     if (CAUSAL && kbase + 32 * t == st.qw0) mask_rows_above(sacc, st.lr - 4 * st.g);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = fast_exp2(fmaf(sacc[i], st.scale_log2, -st.lse2));
+      const float p = PRE ? fast_exp2(sacc[i]) : fast_exp2(fmaf(sacc[i], st.scale_log2, -st.lse2));
       sacc[i] = p * pacc[i];  // dS^T = P^T (dP^T - Delta)
     }
 #pragma unroll
@@ -1009,6 +1037,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     if (my_q < L && st.g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
 #pragma unroll
     for (int i = 0; i < 16; ++i) st.neg_delta[i] = -dl;
+    if constexpr (dq_prescale<T>()) {
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) st.qf[s] = scale_frag<T>(st.qf[s], scale_log2);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st.neg_lse[i] = -st.lse2;
+    }
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) st.koff[s] = swz_off<D>(st.lr, 2 * s + st.g);
 #pragma unroll

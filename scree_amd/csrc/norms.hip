@@ -114,19 +114,22 @@ __global__ __launch_bounds__(fwd_threads<fwd_waves<LAYER>()>()) void norm_fwd_ve
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
           const float d = elem<T>(v[c], e) - mu;
-          s2 += d * d;
+          s2 = __builtin_fmaf(d, d, s2);
         }
       }
     }
     rstd = 1.0f / sqrtf(wave_sum(s2) / fdim + eps);
   } else {
+    // Explicit fused multiply-adds fix the rounding of every step, so the
+    // add + RMSNorm and the plain RMSNorm instantiations (where the compiler
+    // could contract a*a + b*b either way) give identical statistics.
     float s = 0.f;
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float t = elem<T>(v[c], e);
-        s += t * t;
+        s = __builtin_fmaf(t, t, s);
       }
     rstd = 1.0f / sqrtf(wave_sum(s) / fdim + eps);
   }
@@ -183,14 +186,14 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void norm_fwd_generic(
     float s2 = 0.f;
     for (int j = lane; j < dim; j += kWave) {
       const float d = at(j) - mu;
-      s2 += d * d;
+      s2 = __builtin_fmaf(d, d, s2);
     }
     rstd = 1.0f / sqrtf(wave_sum(s2) / fdim + eps);
   } else {
     float s = 0.f;
     for (int j = lane; j < dim; j += kWave) {
       const float t = at(j);
-      s += t * t;
+      s = __builtin_fmaf(t, t, s);
     }
     rstd = 1.0f / sqrtf(wave_sum(s) / fdim + eps);
   }
