@@ -228,6 +228,144 @@ __global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __re
   }
 }
 
+// ------------------------------------------------- wave-level scheduler
+// A batch of at most kWaveSched sequences fits one wavefront, lane s holding
+// sequence s, and any item of either list follows from per-lane registers:
+//  * causal (at most kMaxClass blocks per sequence): class c = blk + 1 from
+//    the largest down, each class in sequence rank order.  Class c starts at
+//    F(c) = sum_s max(0, nblk_s - c) and holds the A(c) sequences with
+//    nblk >= c, which are exactly ranks 0 .. A(c) - 1;
+//  * causal with a longer sequence: natural order (sequence by sequence);
+//  * non-causal: sequences in rank order, blocks ascending;
+//  * sequence-major (second list): rank order, blocks from the last down.
+// attn_wave_schedule_kernel gives every item a wavefront of its own, which
+// works it out with register and DPP operations only: no LDS, no barrier.
+// The scheduler sits on the critical path of every attention step, and the
+// one-block kernel above spends ~4 us there in barriers and LDS round trips.
+constexpr int kWaveSched = 64;
+
+// Wave-uniform sum / maximum of an int over the 64 lanes (all active): four
+// DPP steps combine each 16-lane row (lane ^ 1, lane ^ 2, then the mirrors
+// across 8 and across 16 lanes, each pairing a lane with one in the other
+// half), and the four row results are read as scalars.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += dpp_i<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_i<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_i<0x141>(v);  // row_half_mirror
+  v += dpp_i<0x140>(v);  // row_mirror
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, dpp_i<0xB1>(v));
+  v = max(v, dpp_i<0x4E>(v));
+  v = max(v, dpp_i<0x141>(v));
+  v = max(v, dpp_i<0x140>(v));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ int first_lane(bool pred) {
+  const unsigned long long m = __ballot(pred);
+  return m ? __builtin_ctzll(m) : 0;
+}
+
+struct WaveSched {
+  int start, len, nb;  // this lane's sequence: clamped start, length, row blocks
+  int rank;            // its position in (-nblk, seq) order
+  int base;            // row blocks of the sequences ranked before it
+  int total, cmax;     // item count and largest nblk (wave-uniform)
+};
+
+// Offsets are clamped as in attn_schedule_kernel; lanes >= batch hold empty
+// sequences, which rank after every real one.
+__device__ __forceinline__ WaveSched wave_sched(const int32_t* __restrict__ cu, int batch,
+                                                int total_tokens) {
+  const int lane = threadIdx.x & (kWave - 1);
+  WaveSched w;
+  int a = 0, b = 0;
+  if (lane < batch) {
+    a = min(max(cu[lane], 0), total_tokens);
+    b = min(max(cu[lane + 1], a), total_tokens);
+  }
+  w.start = a;
+  w.len = b - a;
+  w.nb = (w.len + kBM - 1) / kBM;
+  w.total = wave_sum_i(w.nb);
+  w.cmax = wave_max_i(w.nb);
+  int rank = 0, base = 0;
+  for (int t = 0; t < batch; ++t) {
+    const int o = __builtin_amdgcn_readlane(w.nb, t);
+    const bool before = o > w.nb || (o == w.nb && t < lane);
+    rank += before ? 1 : 0;
+    base += before ? o : 0;
+  }
+  w.rank = rank;
+  w.base = base;
+  return w;
+}
+
+// Item p (< w.total) of the work-order list (seq_major false) or of the
+// sequence-major list, as {seq, blk, start, len}.
+__device__ __forceinline__ int4 wave_item(const WaveSched& w, int batch, bool causal,
+                                          bool seq_major, int p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool real = lane < batch;
+  int s, b;
+  if (!seq_major && causal && w.cmax <= kMaxClass) {
+    int lo = 1, hi = w.cmax;  // the smallest class c with F(c) <= p (F falls with c)
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (wave_sum_i(max(0, w.nb - mid)) <= p)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    const int r = p - wave_sum_i(max(0, w.nb - lo));
+    s = first_lane(real && w.rank == r);
+    b = lo - 1;
+  } else if (!seq_major && causal) {
+    const int incl = wave_incl_scan(w.nb);
+    const int nat = incl - w.nb;
+    s = first_lane(real && nat <= p && p < incl);
+    b = p - __builtin_amdgcn_readlane(nat, s);
+  } else {
+    s = first_lane(real && w.base <= p && p < w.base + w.nb);
+    const int j = p - __builtin_amdgcn_readlane(w.base, s);
+    b = seq_major ? __builtin_amdgcn_readlane(w.nb, s) - 1 - j : j;
+  }
+  return make_int4(s, b, __builtin_amdgcn_readlane(w.start, s), __builtin_amdgcn_readlane(w.len, s));
+}
+
+// The two lists and the header for a batch of at most kWaveSched sequences:
+// wave g of the grid writes item g of both lists (grid: tmax waves).
+__global__ __launch_bounds__(256) void attn_wave_schedule_kernel(const int32_t* __restrict__ cu,
+                                                                 int batch, int total_tokens,
+                                                                 int causal, int tmax,
+                                                                 int32_t* __restrict__ header,
+                                                                 int4* __restrict__ items) {
+  const WaveSched w = wave_sched(cu, batch, total_tokens);
+  const bool fits = w.total <= tmax;
+  const int p = blockIdx.x * (blockDim.x / kWave) + (int)(threadIdx.x / kWave);
+  if (fits && p < w.total) {
+    const int4 a = wave_item(w, batch, causal != 0, false, p);
+    const int4 c = wave_item(w, batch, causal != 0, true, p);
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+      items[p] = a;
+      items[tmax + p] = c;
+    }
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    header[0] = fits ? w.total : 0;
+    header[1] = fits ? batch : -1;
+    header[2] = kBM;
+    header[3] = causal;
+  }
+}
+
 // ------------------------------------------------------- tile staging
 // Raw buffer resource for `bytes` bytes at `base` (gfx9 descriptor: stride 0,
 // dword3 = 0x00020000).  Loads at offsets past `bytes` return zeros.
@@ -1627,9 +1765,17 @@ extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t
                      workspace ? workspace_bytes : (size_t)0);
   int32_t* header = static_cast<int32_t*>(workspace);
   int4* items = reinterpret_cast<int4*>(static_cast<char*>(workspace) + kHeaderBytes);
-  hipLaunchKernelGGL(attn_schedule_kernel, dim3(1), dim3(1024), 0,
-                     static_cast<hipStream_t>(stream), cu_seqlens, batch, (int)total_tokens,
-                     causal ? 1 : 0, (int)tmax_for(batch, total_tokens), header, items);
+  const int tmax = (int)tmax_for(batch, total_tokens);
+  if (batch <= kWaveSched) {  // one wavefront per list slot
+    const int waves = 256 / kWave;
+    hipLaunchKernelGGL(attn_wave_schedule_kernel, dim3((unsigned)((tmax + waves - 1) / waves)),
+                       dim3(256), 0, static_cast<hipStream_t>(stream), cu_seqlens, batch,
+                       (int)total_tokens, causal ? 1 : 0, tmax, header, items);
+  } else {
+    hipLaunchKernelGGL(attn_schedule_kernel, dim3(1), dim3(1024), 0,
+                       static_cast<hipStream_t>(stream), cu_seqlens, batch, (int)total_tokens,
+                       causal ? 1 : 0, tmax, header, items);
+  }
   return check_launch(fn);
 }
 

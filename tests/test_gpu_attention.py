@@ -167,6 +167,18 @@ def test_empty_sequences_in_batch():
     _run_case([0, 70, 0, 0, 130, 0], 2, 64, torch.float16, True)
 
 
+@pytest.mark.parametrize("batch", [64, 65, 130])
+@pytest.mark.parametrize("causal", [True, False])
+def test_batches_past_one_wavefront(batch, causal):
+    """Batches past one wavefront of sequences (the scheduler's sort and
+    scans then span several waves), with empty and multi-block sequences."""
+    rng = np.random.default_rng(batch)
+    lengths = [int(x) for x in rng.integers(0, 300, size=batch)]
+    lengths[3] = 0
+    lengths[-1] = 400
+    _run_case(lengths, 2, 64, torch.float16, causal, seed=batch)
+
+
 def test_config3_fixed_list_fp16_causal():
     c = workloads.config3(fixed=True)
     _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=3)
