@@ -69,7 +69,10 @@ const char* scree_last_error(void);
  */
 
 /* Bytes of workspace scree_attn_schedule needs for `batch` sequences holding
- * `total_tokens` tokens in all (independent of heads and causality). */
+ * `total_tokens` tokens in all (independent of heads and causality): a
+ * 16-byte header and two lists of ceil(total_tokens / 128) + batch 16-byte
+ * items, plus, past 2048 sequences (where the lists keep natural order),
+ * batch + 1 prefix sums rounded up to 16 bytes. */
 size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim);
 
 /* Workspace bytes that let the grouped-query backward split each K/V head's
@@ -156,7 +159,8 @@ int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, flo
  * on `stream` (as scree_attn_schedule would) into a static device array of
  * SCREE_ATTN_NOALLOC_SCHEDULE_BYTES per GPU, which holds
  * scree_attn_workspace_bytes() up to that size: 2 * (ceil(total_tokens / 128)
- * + batch) * 16 + 16 bytes, i.e. about 8 million tokens.  Larger problems get
+ * + batch) * 16 + 16 bytes (plus the prefix sums past 2048 sequences), i.e.
+ * about 8 million tokens.  Larger problems get
  * SCREE_ERR_UNSUPPORTED before anything is launched.  Calls no allocating
  * routine.  Calls that overlap on one GPU (several streams or host threads)
  * race on the array; serialise them. */

@@ -41,17 +41,19 @@ def seq_order(nblk) -> list:
     return sorted(range(len(nblk)), key=lambda s: (-int(nblk[s]), s))
 
 
-def build_schedule(offsets, block: int, causal: bool, max_class: int = 4096) -> np.ndarray:
+def build_schedule(offsets, block: int, causal: bool, max_class: int = 4096,
+                   max_batch: int = 2048) -> np.ndarray:
     """Return an ``(T, 2)`` int32 array of ``(seq, blk)`` items.
 
     ``max_class`` is the device scheduler's limit on row blocks per sequence
-    for the causal ordering; past it the list falls back to natural order
-    (sequence by sequence, blocks ascending).
+    for the causal ordering, ``max_batch`` its limit on sequences for any
+    ordering; past either the list falls back to natural order (sequence by
+    sequence, blocks ascending).
     """
     nblk = block_counts(offsets, block)
     order = seq_order(nblk)
     items = []
-    if causal and len(nblk) and int(nblk.max()) > max_class:
+    if len(nblk) > max_batch or (causal and len(nblk) and int(nblk.max()) > max_class):
         for s in range(len(nblk)):
             for b in range(int(nblk[s])):
                 items.append((s, b))
@@ -73,10 +75,12 @@ def item_cost(item, nblk, causal: bool) -> int:
     return b + 1 if causal else int(nblk[s])
 
 
-def build_schedule_by_sequence(offsets, block: int) -> np.ndarray:
+def build_schedule_by_sequence(offsets, block: int, max_batch: int = 2048) -> np.ndarray:
     """The sequence-major list: ``(seq, blk)`` for sequences in ``(-nblk, seq)``
-    rank order, each sequence's blocks ``nblk - 1`` down to ``0``."""
+    rank order (index order past ``max_batch`` sequences), each sequence's
+    blocks ``nblk - 1`` down to ``0``."""
     nblk = block_counts(offsets, block)
-    items = [(s, b) for s in seq_order(nblk) for b in range(int(nblk[s]) - 1, -1, -1)]
+    seqs = range(len(nblk)) if len(nblk) > max_batch else seq_order(nblk)
+    items = [(s, b) for s in seqs for b in range(int(nblk[s]) - 1, -1, -1)]
     return np.asarray(items, dtype=np.int32).reshape(-1, 2)
 

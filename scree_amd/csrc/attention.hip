@@ -39,7 +39,7 @@ constexpr int kWave = 64;
 constexpr int kThreads = 256;   // 4 wavefronts
 constexpr int kBM = 128;        // rows per item (4 waves x 32)
 constexpr int kBN = 64;         // keys per staged block (forward, dQ)
-constexpr int kMaxBatch = 2048; // sequences the scheduler handles
+constexpr int kMaxBatch = 2048; // sequences the sorting scheduler handles (more: natural order)
 constexpr int kMaxClass = 4096; // row blocks per sequence it sorts (longer: natural order)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
@@ -56,6 +56,10 @@ constexpr size_t kHeaderBytes = 16;
 
 inline int64_t tmax_for(int batch, int64_t total) { return (total + kBM - 1) / kBM + batch; }
 inline size_t schedule_bytes(int64_t tmax) { return kHeaderBytes + 2 * (size_t)tmax * sizeof(int4); }
+// Past kMaxBatch the workspace also holds batch + 1 prefix sums after the lists.
+inline size_t prefix_bytes(int batch) {
+  return batch > kMaxBatch ? (((size_t)batch + 1) * sizeof(int32_t) + 15) & ~(size_t)15 : 0;
+}
 
 // ------------------------------------------------------------ scheduler
 __device__ int wave_incl_scan(int v) {
@@ -360,6 +364,74 @@ __global__ __launch_bounds__(256) void attn_wave_schedule_kernel(const int32_t* 
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     header[0] = fits ? w.total : 0;
+    header[1] = fits ? batch : -1;
+    header[2] = kBM;
+    header[3] = causal;
+  }
+}
+
+// ------------------------------------------------- batches past kMaxBatch
+// More sequences than attn_schedule_kernel's LDS arrays hold.  One
+// 1024-thread block writes both lists in natural order instead: sequence by
+// sequence, blocks ascending in the first list and from the last down in the
+// second.  The per-sequence block prefix sums go to a tail of the workspace
+// after the two lists (batch + 1 ints).  Only the balance of a launch, not its
+// result, depends on the longest-first order, and batches this large are
+// made of short sequences.
+__global__ __launch_bounds__(1024) void attn_big_schedule_kernel(
+    const int32_t* __restrict__ cu, int batch, int total_tokens, int causal, int tmax,
+    int32_t* __restrict__ header, int4* __restrict__ items, int32_t* __restrict__ prefix) {
+  __shared__ int s_wtot[16];
+  __shared__ int s_run;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int nw = blockDim.x / kWave;
+  if (tid == 0) s_run = 0;
+  __syncthreads();
+  for (int c0 = 0; c0 < batch; c0 += blockDim.x) {  // exclusive scan of nblk, chunk by chunk
+    const int s = c0 + tid;
+    int nb = 0;
+    if (s < batch) {
+      const int a = min(max(cu[s], 0), total_tokens);
+      const int b = min(max(cu[s + 1], a), total_tokens);
+      nb = (b - a + kBM - 1) / kBM;
+    }
+    const int incl = wave_incl_scan(nb);
+    if (lane == kWave - 1) s_wtot[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+      int t = lane < nw ? s_wtot[lane] : 0;
+      t = wave_incl_scan(t);
+      if (lane < nw) s_wtot[lane] = t;
+    }
+    __syncthreads();
+    if (s < batch) prefix[s] = s_run + (wave > 0 ? s_wtot[wave - 1] : 0) + incl - nb;
+    __syncthreads();  // every thread has read s_run and s_wtot
+    if (tid == 0) s_run += s_wtot[nw - 1];
+    __syncthreads();
+  }
+  const int total = s_run;
+  if (tid == 0) prefix[batch] = total;
+  __threadfence();  // the prefix sums, written by every thread, are read by any
+  __syncthreads();
+  const bool fits = total <= tmax;
+  for (int i = tid; fits && i < total; i += blockDim.x) {
+    int lo = 0, hi = batch - 1;  // the last sequence s with prefix[s] <= i (skips empty ones)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (prefix[mid] <= i)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int s = lo, b = i - prefix[s], nb = prefix[s + 1] - prefix[s];
+    const int a = min(max(cu[s], 0), total_tokens);
+    const int e = min(max(cu[s + 1], a), total_tokens);
+    const int4 it = make_int4(s, b, a, e - a);
+    items[i] = it;
+    items[tmax + prefix[s] + nb - 1 - b] = it;
+  }
+  if (tid == 0) {
+    header[0] = fits ? total : 0;
     header[1] = fits ? batch : -1;
     header[2] = kBM;
     header[3] = causal;
@@ -1591,9 +1663,7 @@ int check_tensor(const char* fn, const char* name, const void* p, const int64_t*
 int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, int heads,
                  int head_dim, int dtype, const void* workspace, size_t workspace_bytes) {
   if (!cu) return set_error(SCREE_ERR_INVALID, "%s: cu_seqlens is null", fn);
-  if (batch < 1 || batch > kMaxBatch)
-    return set_error(SCREE_ERR_UNSUPPORTED, "%s: batch must be in [1, %d], got %d", fn, kMaxBatch,
-                     batch);
+  if (batch < 1) return set_error(SCREE_ERR_UNSUPPORTED, "%s: batch must be at least 1, got %d", fn, batch);
   if (total < 0 || total > ((int64_t)1 << 30))
     return set_error(SCREE_ERR_INVALID, "%s: total_tokens %lld out of range", fn, (long long)total);
   if (heads < 1 || heads > 4096)
@@ -1742,7 +1812,7 @@ using namespace scree;
 extern "C" size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim) {
   (void)head_dim;
   if (batch < 1 || total_tokens < 0) return 0;
-  return schedule_bytes(tmax_for(batch, total_tokens));
+  return schedule_bytes(tmax_for(batch, total_tokens)) + prefix_bytes(batch);
 }
 
 extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_tokens,
@@ -1750,9 +1820,7 @@ extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t
                                    size_t workspace_bytes, void* stream) {
   const char* fn = "scree_attn_schedule";
   if (!cu_seqlens) return set_error(SCREE_ERR_INVALID, "%s: cu_seqlens is null", fn);
-  if (batch < 1 || batch > kMaxBatch)
-    return set_error(SCREE_ERR_UNSUPPORTED, "%s: batch must be in [1, %d], got %d", fn, kMaxBatch,
-                     batch);
+  if (batch < 1) return set_error(SCREE_ERR_UNSUPPORTED, "%s: batch must be at least 1, got %d", fn, batch);
   if (total_tokens < 0 || total_tokens > ((int64_t)1 << 30))
     return set_error(SCREE_ERR_INVALID, "%s: total_tokens %lld out of range", fn,
                      (long long)total_tokens);
@@ -1771,10 +1839,15 @@ extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t
     hipLaunchKernelGGL(attn_wave_schedule_kernel, dim3((unsigned)((tmax + waves - 1) / waves)),
                        dim3(256), 0, static_cast<hipStream_t>(stream), cu_seqlens, batch,
                        (int)total_tokens, causal ? 1 : 0, tmax, header, items);
-  } else {
+  } else if (batch <= kMaxBatch) {
     hipLaunchKernelGGL(attn_schedule_kernel, dim3(1), dim3(1024), 0,
                        static_cast<hipStream_t>(stream), cu_seqlens, batch, (int)total_tokens,
                        causal ? 1 : 0, tmax, header, items);
+  } else {
+    int32_t* prefix = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + schedule_bytes(tmax));
+    hipLaunchKernelGGL(attn_big_schedule_kernel, dim3(1), dim3(1024), 0,
+                       static_cast<hipStream_t>(stream), cu_seqlens, batch, (int)total_tokens,
+                       causal ? 1 : 0, tmax, header, items, prefix);
   }
   return check_launch(fn);
 }

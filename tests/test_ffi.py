@@ -72,6 +72,10 @@ def test_workspace_sizes():
     # header + two lists of (ceil(N/128) + B) int4 items
     assert lib.scree_attn_workspace_bytes(16, 12160, 64) == 16 + 2 * 16 * (95 + 16)
     assert lib.scree_attn_workspace_bytes(0, 10, 64) == 0
+    # past 2048 sequences the (natural-order) scheduler keeps batch + 1
+    # prefix sums after the lists, rounded up to 16 bytes
+    lists = 16 + 2 * 16 * (24 + 3000)
+    assert lib.scree_attn_workspace_bytes(3000, 3000, 64) == lists + 12004 + 12
     assert lib.scree_norm_bwd_workspace_bytes(19758, 4096) == 512 * 2 * 4096 * 4
     assert lib.scree_norm_bwd_workspace_bytes(10, 100) == 2 * 2 * 100 * 4
 

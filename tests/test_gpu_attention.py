@@ -179,6 +179,16 @@ def test_batches_past_one_wavefront(batch, causal):
     _run_case(lengths, 2, 64, torch.float16, causal, seed=batch)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_batch_past_the_sorting_scheduler(causal):
+    """2,500 sequences (beyond the 2,048 the sorting scheduler holds in LDS):
+    the lists come in natural order, with empty and multi-block sequences."""
+    rng = np.random.default_rng(2500)
+    lengths = [int(x) for x in rng.integers(0, 12, size=2500)]
+    lengths[10] = 300
+    _run_case(lengths, 2, 64, torch.float16, causal, seed=25)
+
+
 def test_config3_fixed_list_fp16_causal():
     c = workloads.config3(fixed=True)
     _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=3)
@@ -277,7 +287,8 @@ def test_schedule_bit_exact(causal):
     from scree_amd.kernels.hip import attention_schedule, schedule_items
 
     cases = [EDGE_LENGTHS, [5], [0, 0, 3], workloads.config3().lengths,
-             workloads.config5().lengths, list(range(1, 2049)), [600000, 5, 200]]
+             workloads.config5().lengths, list(range(1, 2049)), [600000, 5, 200],
+             [int(x) for x in np.random.default_rng(7).integers(0, 300, size=3000)]]
     for lengths in cases:
         say(f"case: schedule B={len(lengths)} N={sum(lengths)} causal={causal}")
         off, cu = cu_of(lengths)

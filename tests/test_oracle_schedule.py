@@ -66,3 +66,19 @@ def test_sequence_major_list_by_hand_and_coverage():
             if a[i, 0] == a[i - 1, 0]:
                 assert a[i, 1] == a[i - 1, 1] - 1
 
+
+
+def test_large_batch_lists_fall_back_to_natural_order():
+    """Past max_batch sequences both lists keep index order: the first by
+    sequence then block ascending, the second by sequence then block
+    descending, covering the same items as the sorted lists would."""
+    from oracle.schedule import build_schedule_by_sequence
+
+    lengths = [300, 0, 100, 200, 129]
+    off = offsets_from_lengths(lengths)
+    for causal in (False, True):
+        items = build_schedule(off, 128, causal, max_batch=4)
+        assert items.tolist() == [[0, 0], [0, 1], [0, 2], [2, 0], [3, 0], [3, 1], [4, 0], [4, 1]]
+        assert build_schedule(off, 128, causal, max_batch=5).tolist() != items.tolist()
+    seq = build_schedule_by_sequence(off, 128, max_batch=4)
+    assert seq.tolist() == [[0, 2], [0, 1], [0, 0], [2, 0], [3, 1], [3, 0], [4, 1], [4, 0]]
