@@ -160,7 +160,10 @@ class AttnCase:
                               device=dev)
 
     def schedule(self):
-        self.A.attention_schedule(self.cu, self.cfg.total, self.cfg.head_dim, self.cfg.causal, self.ws)
+        """The work list, as the user-facing calls build it (nothing for a
+        launch small enough that its workgroups derive their own items)."""
+        self.A.prepare_workspace(self.cu, self.cfg.total, self.cfg.head_dim, self.cfg.causal,
+                                 self.cfg.heads, self.ws)
 
     def fwd(self):
         self.A._attn_fwd(self.q, self.k, self.v, self.cu, self.cfg.causal, self.out, self.lse, self.ws)

@@ -75,6 +75,16 @@ const char* scree_last_error(void);
  * batch + 1 prefix sums rounded up to 16 bytes. */
 size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim);
 
+/* 1 when the attention calls for this problem read the work list
+ * scree_attn_schedule writes; 0 when every workgroup derives its own item
+ * from cu_seqlens instead (at most 64 sequences and at most 1024 workgroups
+ * per launch, i.e. (ceil(total_tokens / 128) + batch) * heads <= 1024: one
+ * round of workgroups, where the scheduler launch would be pure latency), so
+ * that the schedule call can be skipped.  The workspace argument of the
+ * attention calls is still required and size-checked.  No counterpart in the
+ * reference. */
+int scree_attn_needs_schedule(int batch, int64_t total_tokens, int heads);
+
 /* Workspace bytes that let the grouped-query backward split each K/V head's
  * group of query heads over several workgroups (>= scree_attn_workspace_bytes;
  * equal to it when heads == kv_heads or the grid already fills the GPU).
@@ -91,7 +101,8 @@ size_t scree_attn_bwd_workspace_bytes_gqa(int batch, int64_t total_tokens, int h
 
 /* Build the longest-work-first tile list for `cu_seqlens` into `workspace`.
  * Must precede scree_attn_fwd / scree_attn_bwd with the same cu_seqlens,
- * head_dim and causal flag; the workspace may then be reused by any number of
+ * head_dim and causal flag when scree_attn_needs_schedule returns 1 (calling
+ * it anyway is harmless); the workspace may then be reused by any number of
  * forward and backward calls.  No counterpart in the reference (its grid is
  * padded, src/scree/kernels/triton/varlen_attention.py:236). */
 int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_tokens,

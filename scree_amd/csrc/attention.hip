@@ -279,8 +279,6 @@ __device__ __forceinline__ int first_lane(bool pred) {
 
 struct WaveSched {
   int start, len, nb;  // this lane's sequence: clamped start, length, row blocks
-  int rank;            // its position in (-nblk, seq) order
-  int base;            // row blocks of the sequences ranked before it
   int total, cmax;     // item count and largest nblk (wave-uniform)
 };
 
@@ -300,24 +298,39 @@ __device__ __forceinline__ WaveSched wave_sched(const int32_t* __restrict__ cu, 
   w.nb = (w.len + kBM - 1) / kBM;
   w.total = wave_sum_i(w.nb);
   w.cmax = wave_max_i(w.nb);
-  int rank = 0, base = 0;
-  for (int t = 0; t < batch; ++t) {
-    const int o = __builtin_amdgcn_readlane(w.nb, t);
-    const bool before = o > w.nb || (o == w.nb && t < lane);
-    rank += before ? 1 : 0;
-    base += before ? o : 0;
-  }
-  w.rank = rank;
-  w.base = base;
   return w;
 }
 
+// The lane of the k-th (from 0, in lane order) lane where pred holds; it must exist.
+__device__ __forceinline__ int nth_lane(bool pred, int k) {
+  const unsigned long long m = __ballot(pred);
+  const int below = (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+  return first_lane(pred && below == k);
+}
+
+// Rank order is nblk descending, ties by sequence index: the sequence of rank
+// r has the largest nblk v with count(nblk >= v) > r and is the
+// (r - count(nblk > v))-th of those holding v.  The caller knows that
+// count(nblk >= lo) > r.  Binary search over v with one ballot a step, in
+// place of comparing every pair of sequences.
+__device__ __forceinline__ int lane_of_rank(const WaveSched& w, int r, int lo) {
+  int hi = w.cmax;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (__popcll(__ballot(w.nb >= mid)) > r)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return nth_lane(w.nb == lo, r - __popcll(__ballot(w.nb > lo)));
+}
+
 // Item p (< w.total) of the work-order list (seq_major false) or of the
-// sequence-major list, as {seq, blk, start, len}.
+// sequence-major list, as {seq, blk, start, len}.  Lanes past the batch hold
+// nblk 0 and are never selected.
 __device__ __forceinline__ int4 wave_item(const WaveSched& w, int batch, bool causal,
                                           bool seq_major, int p) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const bool real = lane < batch;
   int s, b;
   if (!seq_major && causal && w.cmax <= kMaxClass) {
     int lo = 1, hi = w.cmax;  // the smallest class c with F(c) <= p (F falls with c)
@@ -328,18 +341,31 @@ __device__ __forceinline__ int4 wave_item(const WaveSched& w, int batch, bool ca
       else
         lo = mid + 1;
     }
-    const int r = p - wave_sum_i(max(0, w.nb - lo));
-    s = first_lane(real && w.rank == r);
+    // class lo holds the sequences of ranks 0 .. count(nblk >= lo) - 1
+    s = lane_of_rank(w, p - wave_sum_i(max(0, w.nb - lo)), lo);
     b = lo - 1;
   } else if (!seq_major && causal) {
+    const int lane = threadIdx.x & (kWave - 1);
     const int incl = wave_incl_scan(w.nb);
     const int nat = incl - w.nb;
-    s = first_lane(real && nat <= p && p < incl);
+    s = first_lane(lane < batch && nat <= p && p < incl);
     b = p - __builtin_amdgcn_readlane(nat, s);
   } else {
-    s = first_lane(real && w.base <= p && p < w.base + w.nb);
-    const int j = p - __builtin_amdgcn_readlane(w.base, s);
-    b = seq_major ? __builtin_amdgcn_readlane(w.nb, s) - 1 - j : j;
+    // sequences in rank order, each nblk items long: the largest v whose
+    // sequences (nblk >= v) cover position p, then p's place among the
+    // sequences holding exactly v
+    int lo = 1, hi = w.cmax;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (wave_sum_i(w.nb >= mid ? w.nb : 0) > p)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int q = p - wave_sum_i(w.nb > lo ? w.nb : 0);
+    const int k = q / lo, j = q - k * lo;
+    s = nth_lane(w.nb == lo, k);
+    b = seq_major ? lo - 1 - j : j;
   }
   return make_int4(s, b, __builtin_amdgcn_readlane(w.start, s), __builtin_amdgcn_readlane(w.len, s));
 }
@@ -368,6 +394,49 @@ __global__ __launch_bounds__(256) void attn_wave_schedule_kernel(const int32_t* 
     header[2] = kBM;
     header[3] = causal;
   }
+}
+
+// ------------------------------------------------- where items come from
+// A launch small enough to run in one round of workgroups (the host decides,
+// attn_derive_items) skips the scheduler launch altogether: every wave of
+// every workgroup derives its own item from cu_seqlens with the code above.
+// That costs each workgroup ~300 instructions before its first load -- a
+// loss when the CUs are full (each workgroup holds its slot longer) but far
+// less than the scheduler launch (~3.5 us of dependent latency) when the
+// launch is latency-bound.  Larger launches read the scheduler's list.
+struct ItemSource {
+  const int32_t* header;
+  const int4* items;  // the list this launch reads
+  const int32_t* cu;
+  int batch, total_tokens;
+  int seq_major;      // the sequence-major list (head-major launches)
+  int derive;         // derive items from cu (batch <= kWaveSched)
+};
+
+// The schedule as this wave sees it: whether it failed (offsets that
+// describe more work than tmax) and the item count.  The header and the
+// listed item are loaded in both modes (the workspace always holds them;
+// stale bytes when deriving) so that on the list path their loads issue
+// with the kernel arguments rather than after a branch on src.derive.
+struct ItemView {
+  WaveSched w;
+  bool failed;
+  int count;
+};
+__device__ __forceinline__ ItemView item_view(const ItemSource& src, int tmax) {
+  const int listed_count = src.header[0], listed_batch = src.header[1];
+  ItemView v;
+  v.w = WaveSched{0, 0, 0, 0, 0};
+  if (src.derive) v.w = wave_sched(src.cu, src.batch, src.total_tokens);
+  v.failed = src.derive ? v.w.total > tmax : listed_batch < 0;
+  v.count = src.derive ? (v.failed ? 0 : v.w.total) : listed_count;
+  return v;
+}
+__device__ __forceinline__ int4 item_at(const ItemSource& src, const ItemView& v, bool causal, int p) {
+  const int4 listed = src.items[p];
+  int4 it = make_int4(0, 0, 0, 0);
+  if (src.derive) it = wave_item(v.w, src.batch, causal, src.seq_major != 0, p);
+  return src.derive ? it : listed;
 }
 
 // ------------------------------------------------- batches past kMaxBatch
@@ -917,26 +986,35 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
   __syncthreads();
 }
 
+// Waves per SIMD the forward is compiled for: four (128 registers) for the
+// causal form up to head_dim 64, which fits them without spills; two
+// otherwise (the compiler then takes what it needs: 134 registers, three
+// waves, for the non-causal form at 64).
+template <int D, bool CAUSAL>
+constexpr int attn_fwd_waves() {
+  return CAUSAL && D <= 64 ? 4 : 2;
+}
+
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
+__global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
-    float* __restrict__ lse, const int32_t* __restrict__ header, const int4* __restrict__ items,
-    int tmax, int head_major, int heads, int group, Strides sq, Strides sk, Strides sv,
-    Strides so, float scale, float scale_log2, int total) {
+    float* __restrict__ lse, ItemSource src, int tmax, int head_major, int heads, int group,
+    Strides sq, Strides sk, Strides sv, Strides so, float scale, float scale_log2, int total) {
   constexpr int TILE = kBN * D;  // elements per K or V tile
   constexpr int BUF = 2 * TILE;  // one buffer: K tile then V tile
   __shared__ __align__(16) T smem[2 * BUF];
   static_assert(4 * stage_elems<D>() <= 2 * BUF, "O staging must fit in the tile buffers");
 
-  if (header[1] < 0) {  // failed schedule
+  const ItemView iv = item_view(src, tmax);
+  if (iv.failed) {
     poison_rows(o, so, total, heads, D);
     poison_stats(lse, total, heads);
     return;
   }
   int item, h;
-  if (!map_block(heads, tmax, head_major, group, item, h) || item >= header[0]) return;
+  if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) return;
   const int hk = h / group;  // K/V head of this query head
-  const int4 it = items[item];
+  const int4 it = item_at(src, iv, CAUSAL, item);
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   FwdState<T, D> st;
   st.wave = wave_id();
@@ -1175,8 +1253,8 @@ template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
-    float* __restrict__ delta, T* __restrict__ dq, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int tmax, int head_major, int heads, int group, Strides sdo,
+    float* __restrict__ delta, T* __restrict__ dq, ItemSource src, int tmax, int head_major,
+    int heads, int group, Strides sdo,
     Strides sq, Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2,
     int total) {
   typedef typename VecT<T>::x8 x8;
@@ -1185,15 +1263,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   __shared__ __align__(16) T smem[dq_nbuf<D>() * BUF];
   static_assert(4 * stage_elems<D>() <= dq_nbuf<D>() * BUF, "dQ staging must fit in the tile buffers");
 
-  if (header[1] < 0) {  // failed schedule
+  const ItemView iv = item_view(src, tmax);
+  if (iv.failed) {
     poison_rows(dq, sdq, total, heads, D);
     poison_stats(delta, total, heads);
     return;
   }
   int item, h;
-  if (!map_block(heads, tmax, head_major, group, item, h) || item >= header[0]) return;
+  if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) return;
   const int hk = h / group;  // K/V head of this query head
-  const int4 it = items[item];
+  const int4 it = item_at(src, iv, CAUSAL, item);
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   DqState<T, D> st;
   st.wave = wave_id();
@@ -1454,14 +1533,14 @@ __device__ __forceinline__ void dkv_store_partial(const f32x16 (&dk)[D / 32],
 constexpr int kRedRows = 16;
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dkv_reduce_kernel(
-    const float* __restrict__ partial, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int kv_heads, int gsplit, T* __restrict__ dk,
-    T* __restrict__ dv, Strides sdk, Strides sdv, float scale) {
+    const float* __restrict__ partial, ItemSource src, int tmax, int causal, int kv_heads,
+    int gsplit, T* __restrict__ dk, T* __restrict__ dv, Strides sdk, Strides sdv, float scale) {
   constexpr int CHUNKS = kBM / kRedRows;
   const int slot = blockIdx.x / CHUNKS, chunk = blockIdx.x % CHUNKS;
   const int item = slot / kv_heads, hk = slot % kv_heads;
-  if (item >= header[0]) return;
-  const int4 it = items[item];
+  const ItemView iv = item_view(src, tmax);  // a failed schedule: the pass poisoned dk / dv
+  if (item >= iv.count) return;
+  const int4 it = item_at(src, iv, causal != 0, item);
   const int start = it.z, L = it.w;
   const int k0 = ((L + kBM - 1) / kBM - 1 - it.y) * kBM;
   constexpr int C4 = D / 4;
@@ -1499,8 +1578,8 @@ template <typename T, int D, bool CAUSAL, bool SPLIT, bool REV>
 __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_dkv_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
-    T* __restrict__ dk, T* __restrict__ dv, const int32_t* __restrict__ header,
-    const int4* __restrict__ items, int tmax, int head_major, int kv_heads, int group,
+    T* __restrict__ dk, T* __restrict__ dv, ItemSource src, int tmax, int head_major,
+    int kv_heads, int group,
     Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk, Strides sdv, float scale,
     float scale_log2, int gsplit, float* __restrict__ partial, int total) {
   constexpr int BQ = dkv_bq<D>();
@@ -1521,17 +1600,18 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   // and their contributions accumulate in the dK / dV registers.  With
   // gsplit > 1 parts, each part stores its fp32 sums and dkv_reduce_kernel
   // adds them up after the pass.
-  if (header[1] < 0) {  // failed schedule
+  const ItemView iv = item_view(src, tmax);
+  if (iv.failed) {
     poison_rows(dk, sdk, total, kv_heads, D);
     poison_rows(dv, sdv, total, kv_heads, D);
     return;
   }
   int item, hv;
-  if (!map_block(kv_heads * gsplit, tmax, head_major, 1, item, hv) || item >= header[0]) return;
+  if (!map_block(kv_heads * gsplit, tmax, head_major, 1, item, hv) || item >= iv.count) return;
   const int hk = hv % kv_heads, part = hv / kv_heads;
   const int g0 = part * group / gsplit, g1 = (part + 1) * group / gsplit;
   const int heads = kv_heads * group;
-  const int4 it = items[item];
+  const int4 it = item_at(src, iv, CAUSAL, item);
   const int start = it.z, L = it.w;
   const int nblk = (L + kBM - 1) / kBM;
   const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
@@ -1722,19 +1802,30 @@ inline const int4* schedule_list(const void* ws, int tmax, int head_major) {
   return reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes) +
          (head_major ? tmax : 0);
 }
+// Launches of at most one round of workgroups (256 CUs x 4) over at most
+// kWaveSched sequences derive their items in the kernels (see ItemSource);
+// the decision depends only on the batch, the token count and the query
+// heads, so every pass of one problem takes the same one.
+constexpr int64_t kDeriveMaxBlocks = 1024;
+inline bool attn_derive_items(int batch, int64_t tmax, int heads) {
+  return batch <= kWaveSched && tmax * heads <= kDeriveMaxBlocks;
+}
+inline ItemSource item_source(const void* ws, const int32_t* cu, int batch, int total, int tmax,
+                              int head_major, int heads) {
+  return ItemSource{static_cast<const int32_t*>(ws), schedule_list(ws, tmax, head_major), cu, batch,
+                    total, head_major, attn_derive_items(batch, tmax, heads) ? 1 : 0};
+}
 
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
-                  const int32_t* /*cu: the items carry the bounds*/, int heads, int kv_heads,
-                  const int64_t* st, float scale, int tmax, const void* ws, int total,
-                  hipStream_t stream) {
+                  const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
+                  float scale, int tmax, const void* ws, int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
-  const int32_t* header = static_cast<const int32_t*>(ws);
   const int hm = attn_head_major(heads, tmax);
-  const int4* items = schedule_list(ws, tmax, hm);
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(o), lse, header, items, tmax, hm,
+                     static_cast<T*>(o), lse, item_source(ws, cu, batch, total, tmax, hm, heads),
+                     tmax, hm,
                      heads, heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
                      Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e, total);
 }
@@ -1742,18 +1833,17 @@ void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* l
 // strides: {dout, q, k, v, o, dq} x {row, head}
 template <typename T, int D, bool C>
 void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
-                     const float* lse, void* dq, float* delta, const int32_t* /*cu*/, int heads,
-                     int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
-                     int total, hipStream_t stream) {
+                     const float* lse, void* dq, float* delta, const int32_t* cu, int batch,
+                     int heads, int kv_heads, const int64_t* st, float scale, int tmax,
+                     const void* ws, int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
-  const int32_t* header = static_cast<const int32_t*>(ws);
   const int hm = attn_head_major(heads, tmax);
-  const int4* items = schedule_list(ws, tmax, hm);
   hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<const T*>(o), lse, delta, static_cast<T*>(dq), header, items,
-                     tmax, hm, heads, heads / kv_heads,
+                     static_cast<const T*>(o), lse, delta, static_cast<T*>(dq),
+                     item_source(ws, cu, batch, total, tmax, hm, heads), tmax, hm, heads,
+                     heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
                      scale * kLog2e, total);
@@ -1762,14 +1852,13 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
 // strides: {dout, q, k, v, dk, dv} x {row, head}
 template <typename T, int D, bool C>
 void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
-                      const float* lse, const float* delta, void* dk, void* dv, const int32_t* /*cu*/,
-                      int heads, int kv_heads, const int64_t* st, float scale, int tmax,
+                      const float* lse, const float* delta, void* dk, void* dv, const int32_t* cu,
+                      int batch, int heads, int kv_heads, const int64_t* st, float scale, int tmax,
                       const void* ws, int gsplit, float* partial, int total, hipStream_t stream) {
   // one workgroup per (item, K/V head, part of the head group)
   const int64_t grid = (int64_t)tmax * kv_heads * gsplit;
-  const int32_t* header = static_cast<const int32_t*>(ws);
   const int hm = attn_head_major(kv_heads * gsplit, tmax);
-  const int4* items = schedule_list(ws, tmax, hm);
+  const ItemSource src = item_source(ws, cu, batch, total, tmax, hm, heads);
   // the split epilogue has a kernel of its own: its registers would cost the
   // unsplit kernel a wave per SIMD at D = 64
   // (a split group never has the many rounds of a head-major launch)
@@ -1779,7 +1868,7 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), lse, delta,
-                     static_cast<T*>(dk), static_cast<T*>(dv), header, items, tmax, hm, kv_heads,
+                     static_cast<T*>(dk), static_cast<T*>(dv), src, tmax, hm, kv_heads,
                      heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
@@ -1787,7 +1876,7 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
   if (gsplit > 1)
     hipLaunchKernelGGL((dkv_reduce_kernel<T, D>),
                        dim3((unsigned)((int64_t)tmax * kv_heads * (kBM / kRedRows))), dim3(256), 0,
-                       stream, partial, header, items, kv_heads, gsplit, static_cast<T*>(dk),
+                       stream, partial, src, tmax, C ? 1 : 0, kv_heads, gsplit, static_cast<T*>(dk),
                        static_cast<T*>(dv), Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale);
 }
 
@@ -1808,6 +1897,11 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
 }  // namespace scree
 
 using namespace scree;
+
+extern "C" int scree_attn_needs_schedule(int batch, int64_t total_tokens, int heads) {
+  if (batch < 1 || total_tokens < 0 || heads < 1) return 1;
+  return attn_derive_items(batch, tmax_for(batch, total_tokens), heads) ? 0 : 1;
+}
 
 extern "C" size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim) {
   (void)head_dim;
@@ -1897,7 +1991,7 @@ static int launch_fwd(const char* fn, const void* q, const void* k, const void* 
                       void* stream) {
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
-  SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, heads,
+  SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, batch, heads,
                  kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
@@ -1975,9 +2069,11 @@ extern "C" int scree_attn_fwd_noalloc(const void* q, const void* k, const void* 
   if (rc) return rc;
   if (total_tokens == 0) return SCREE_OK;
   if ((rc = scratch_for_current_device(fn, &ws))) return rc;
-  rc = scree_attn_schedule(cu_seqlens, batch, total_tokens, head_dim, causal, ws,
-                           SCREE_ATTN_NOALLOC_SCHEDULE_BYTES, stream);
-  if (rc) return rc;
+  if (scree_attn_needs_schedule(batch, total_tokens, heads)) {
+    rc = scree_attn_schedule(cu_seqlens, batch, total_tokens, head_dim, causal, ws,
+                             SCREE_ATTN_NOALLOC_SCHEDULE_BYTES, stream);
+    if (rc) return rc;
+  }
   return launch_fwd(fn, q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, kv_heads,
                     head_dim, strides, softmax_scale, causal, dtype, ws, stream);
 }
@@ -2014,7 +2110,7 @@ extern "C" int scree_attn_bwd_dq_gqa(const void* dout, const void* q, const void
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
-                 cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace,
+                 cu_seqlens, batch, heads, kv_heads, strides, softmax_scale, tmax, workspace,
                  (int)total_tokens, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
@@ -2061,7 +2157,7 @@ extern "C" int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const voi
                                     static_cast<char*>(const_cast<void*>(workspace)) + base)
                               : nullptr;
   SCREE_DISPATCH(launch_bwd_dkv_t, dtype, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
-                 cu_seqlens, heads, kv_heads, strides, softmax_scale, tmax, workspace, gsplit,
+                 cu_seqlens, batch, heads, kv_heads, strides, softmax_scale, tmax, workspace, gsplit,
                  partial, (int)total_tokens, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }

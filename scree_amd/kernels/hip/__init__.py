@@ -16,6 +16,8 @@ from ._autograd import VarlenAttentionHip, varlen_attention_hip_autograd
 from ._ffi import HIP_AVAILABLE, HipUnavailableError, ScreeHipError
 from .attention import (
     attention_schedule,
+    needs_schedule,
+    prepare_workspace,
     schedule_items,
     varlen_attention_hip,
     varlen_attention_hip_backward,
@@ -50,6 +52,8 @@ __all__ = [
     "ScreeHipError",
     "VarlenAttentionHip",
     "attention_schedule",
+    "needs_schedule",
+    "prepare_workspace",
     "schedule_items",
     "varlen_add_rmsnorm_hip",
     "varlen_add_rmsnorm_hip_backward",

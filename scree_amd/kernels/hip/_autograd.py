@@ -6,7 +6,8 @@ Mirrors ``varlen_attention_triton_autograd``
 None)``.  Two differences: the Function class is defined once at import
 (the reference rebuilds it on every call, ``_autograd.py:71``), and the
 forward also keeps the device work list it built (schedule-sized: 16 bytes
-per 128-token block plus 16 per sequence), so the backward launches no
+per 128-token block plus 16 per sequence; small launches need no list, their
+workgroups derive their items from the offsets), so the backward launches no
 scheduler and never synchronises the host.  When the grouped-query dK/dV
 split pays, the backward allocates the larger workspace it needs for the
 duration of the pass and copies the work list into it on the device.
@@ -29,7 +30,7 @@ class VarlenAttentionHip(torch.autograd.Function):
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         lse = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
         with torch.cuda.device(q.device):
-            ws = _attn.attention_schedule(cu, total, head_dim, causal)
+            ws = _attn.prepare_workspace(cu, total, head_dim, causal, n_heads)
             _attn._attn_fwd(qk, kk, vk, cu, causal, out, lse, ws)
         ctx.save_for_backward(qk, kk, vk, out, lse, cu, ws)
         ctx.causal = causal

@@ -82,6 +82,28 @@ def workspace_bytes(batch: int, total: int, head_dim: int) -> int:
     return int(_ffi.lib().scree_attn_workspace_bytes(batch, total, head_dim))
 
 
+def needs_schedule(batch: int, total: int, heads: int) -> bool:
+    """Whether the kernels read the work list of :func:`attention_schedule`.
+    Small launches (at most 64 sequences and one round of workgroups) derive
+    their items from ``cu_seqlens`` inside every workgroup instead, which
+    saves the scheduler launch's latency."""
+    return bool(_ffi.lib().scree_attn_needs_schedule(batch, total, heads))
+
+
+def prepare_workspace(cu_seqlens: torch.Tensor, total_tokens: int, head_dim: int, causal: bool,
+                      heads: int, workspace: torch.Tensor = None) -> torch.Tensor:
+    """A workspace the attention calls accept for these offsets and heads:
+    the work list built into it when the launches read one, else the room
+    alone (allocated when ``workspace`` is None)."""
+    batch = cu_seqlens.numel() - 1
+    if needs_schedule(batch, total_tokens, heads):
+        return attention_schedule(cu_seqlens, total_tokens, head_dim, causal, workspace)
+    if workspace is None:
+        workspace = torch.empty(workspace_bytes(batch, total_tokens, head_dim), dtype=torch.uint8,
+                                device=cu_seqlens.device)
+    return workspace
+
+
 def bwd_workspace_bytes(batch: int, total: int, heads: int, kv_heads: int, head_dim: int) -> int:
     """Workspace bytes for a forward + backward with ``kv_heads`` K/V heads:
     the schedule, plus room for the grouped-query dK/dV split when it pays."""
@@ -185,7 +207,8 @@ def varlen_attention_hip(q, k, v, cu_seqlens, causal: bool = False, block_m: int
     ``(total_tokens, n_heads, head_dim)`` fp16/bf16 device tensors,
     ``cu_seqlens`` the int32 ``(batch + 1,)`` offsets.  ``out`` /
     ``lse_buffer`` are optional preallocated outputs.  ``workspace`` is an
-    optional schedule from :func:`attention_schedule` for these offsets.
+    optional workspace from :func:`prepare_workspace` (or a schedule from
+    :func:`attention_schedule`) for these offsets.
 
     Returns ``out`` or ``(out, lse)`` with ``lse`` the natural-log
     logsumexp of the scaled scores, ``(total_tokens, n_heads)`` fp32.
@@ -209,7 +232,7 @@ def varlen_attention_hip(q, k, v, cu_seqlens, causal: bool = False, block_m: int
     ok = _kernel_view(out)
     with torch.cuda.device(q.device):
         if workspace is None:
-            workspace = attention_schedule(cu, total, head_dim, causal)
+            workspace = prepare_workspace(cu, total, head_dim, causal, n_heads)
         _attn_fwd(qk, kk, vk, cu, causal, ok, lse, workspace)
     if ok is not out:
         out.copy_(ok)
@@ -248,7 +271,7 @@ def varlen_attention_hip_backward(do, q, k, v, o, lse, cu_seqlens, causal: bool 
     ins = [_kernel_view(t) for t in (do, q, k, v, o)]
     with torch.cuda.device(q.device):
         if workspace is None:
-            workspace = attention_schedule(cu, total, head_dim, causal,
-                                           _bwd_workspace(cu, total, n_heads, k.shape[1], head_dim))
+            workspace = prepare_workspace(cu, total, head_dim, causal, n_heads,
+                                          _bwd_workspace(cu, total, n_heads, k.shape[1], head_dim))
         _attn_bwd(*ins, lse.contiguous(), cu, causal, dq, dk, dv, delta, workspace)
     return dq, dk, dv

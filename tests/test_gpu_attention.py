@@ -189,6 +189,57 @@ def test_batch_past_the_sorting_scheduler(causal):
     _run_case(lengths, 2, 64, torch.float16, causal, seed=25)
 
 
+def test_small_launch_reads_no_work_list():
+    """A launch small enough to derive its items from the offsets gives the
+    same outputs, bit for bit, with a workspace of stale bytes."""
+    from scree_amd.kernels.hip import (needs_schedule, varlen_attention_hip,
+                                       varlen_attention_hip_backward)
+    from scree_amd.kernels.hip import attention as A
+
+    lengths = [300, 17, 129, 640, 1, 0, 77]
+    n = sum(lengths)
+    say(f"case: stale workspace B={len(lengths)} N={n} H=4")
+    assert not needs_schedule(len(lengths), n, 4)
+    off, cu = cu_of(lengths)
+    q, k, v, do = (randn((n, 4, 64), torch.float16, 50 + i) for i in range(4))
+    ref = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+    ref_g = varlen_attention_hip_backward(do, q, k, v, ref[0], ref[1], cu, causal=True)
+    stale = torch.full((A.workspace_bytes(len(lengths), n, 64),), 255, dtype=torch.uint8,
+                       device="cuda")
+    got = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True, workspace=stale)
+    got_g = varlen_attention_hip_backward(do, q, k, v, got[0], got[1], cu, causal=True,
+                                          workspace=stale)
+    torch.cuda.synchronize()
+    assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
+    for a, b in zip(ref_g, got_g):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_derived_and_listed_items_agree(causal):
+    """Heads are independent: config 4's lengths at 16 heads (1,776
+    workgroups, read from the scheduler's list) and the first 4 of those heads
+    alone (444 workgroups, items derived in the kernels) give the same
+    outputs and gradients for those heads, bit for bit."""
+    from scree_amd.kernels.hip import needs_schedule, varlen_attention_hip, varlen_attention_hip_backward
+
+    c = workloads.config4()
+    n = sum(c.lengths)
+    say(f"case: derived vs listed items, config 4 lengths, causal={causal}")
+    assert needs_schedule(len(c.lengths), n, 16) and not needs_schedule(len(c.lengths), n, 4)
+    off, cu = cu_of(c.lengths)
+    q, k, v, do = (randn((n, 16, 64), torch.float16, 60 + i) for i in range(4))
+    o16, l16 = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True)
+    g16 = varlen_attention_hip_backward(do, q, k, v, o16, l16, cu, causal=causal)
+    sub = [t[:, :4].contiguous() for t in (q, k, v, do)]
+    o4, l4 = varlen_attention_hip(*sub[:3], cu, causal=causal, return_lse=True)
+    g4 = varlen_attention_hip_backward(sub[3], *sub[:3], o4, l4, cu, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(o16[:, :4], o4) and torch.equal(l16[:, :4], l4)
+    for a, b in zip(g16, g4):
+        assert torch.equal(a[:, :4], b)
+
+
 def test_config3_fixed_list_fp16_causal():
     c = workloads.config3(fixed=True)
     _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=3)
@@ -288,6 +339,8 @@ def test_schedule_bit_exact(causal):
 
     cases = [EDGE_LENGTHS, [5], [0, 0, 3], workloads.config3().lengths,
              workloads.config5().lengths, list(range(1, 2049)), [600000, 5, 200],
+             # one wave of sequences, most sharing a block count (ties by index)
+             [int(x) for x in np.random.default_rng(9).integers(0, 4, size=60) * 100],
              [int(x) for x in np.random.default_rng(7).integers(0, 300, size=3000)]]
     for lengths in cases:
         say(f"case: schedule B={len(lengths)} N={sum(lengths)} causal={causal}")
