@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of the HIP varlen kernel path on one MI355X.
 
-``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]``
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms MS] [--no-cpu] [--only NAME]``
 
 Primary line: causal varlen attention forward +
 backward, fp16, 16 sequences summing to 12160 tokens (log-normal, sigma 0.6,
@@ -9,7 +9,13 @@ rescaled), 16 heads x head_dim 64, synthetic N(0,1) inputs already resident
 in HBM.  One step = tile scheduler + forward (O, LSE) + dQ/Delta pass + dK/dV
 pass into preallocated buffers.  K steps are replayed from HIP graphs of up
 to 10 consecutive steps (graphs of one step and eager call-by-call launches
-are reported beside it).  ``value`` is real-token causal TFLOP/s
+are reported beside it).  Every timed region is preceded by untimed
+repetitions of exactly what it times (the same launches, or the same graph
+replays) for ``--settle-ms`` milliseconds (default 50, recorded in
+``config.settle_ms``): after any idle spell -- process start, or host-only
+work such as graph capture -- the GPU runs its first ~10-20 ms of work up to
+17 % slower while its clocks ramp up, which would otherwise land in a timed
+region that lasts ~8 ms.  ``value`` is real-token causal TFLOP/s
 (4*H*D*sum L(L+1)/2 forward, x3.5 for forward+backward).
 
 Also reported (``secondary``): config 3 forward, config 4 on the reference's
@@ -48,12 +54,29 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+SETTLE_S = 0.05  # set from --settle-ms
+
+
+def _settle(fn) -> None:
+    """Untimed calls of ``fn`` (the very thing the next timed region runs)
+    for SETTLE_S seconds of wall time, synchronising every 8 calls so that the
+    host never runs far ahead of the GPU.  A GPU that has been idle runs its
+    first ~10-20 ms of work up to 17 % slower while its clocks ramp up."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
 def _events_time(fn, reps: int) -> float:
     """Average milliseconds of ``fn`` over ``reps`` back-to-back calls (HIP events)."""
     import torch
 
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    _settle(fn)
     start.record()
     for _ in range(reps):
         fn()
@@ -80,7 +103,7 @@ def _graph_time(fn, reps: int, replays: int) -> float:
         for _ in range(reps):
             fn()
     graph.replay()
-    torch.cuda.synchronize()
+    _settle(graph.replay)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(replays):
@@ -120,7 +143,7 @@ def _graph_steps_time(fn, steps: int, chunk: int = 10) -> float:
     for g in (g_full, g_rem):
         if g is not None:
             g.replay()
-    torch.cuda.synchronize()
+    _settle((g_full or g_rem).replay)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(full):
@@ -202,14 +225,7 @@ def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False, kv_hea
     step = case.step_fwd_bwd if backward else case.step_fwd
     for _ in range(warmup):
         step()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    eager_ms = start.elapsed_time(end) / steps
+    eager_ms = _events_time(step, steps)
     graph1_ms = _graph_time(step, 1, steps)
     ms = _graph_steps_time(step, steps)
     flops = cfg.fwd_flops() * (3.5 if backward else 1.0)
@@ -519,6 +535,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--primary-only", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-sweep", action="store_true", help="skip the 27-shape sweep")
+    ap.add_argument("--settle-ms", type=float, default=50.0, metavar="MS",
+                    help="untimed repetitions of each timed region's launches before it (0: none)")
     ap.add_argument("--only", choices=["cfg5"], default=None,
                     help="time one secondary workload alone and print its figures (for profiling)")
     args = ap.parse_args()
@@ -538,6 +556,8 @@ def main() -> int:
     _ffi.lib()  # raise now if the library is missing
     torch.cuda.set_device(0)
     fp16 = torch.float16
+    global SETTLE_S
+    SETTLE_S = max(0.0, args.settle_ms) * 1e-3
     if args.only == "cfg5":
         cfg5 = workloads.config5()
         r, _ = time_attention(cfg5, torch.bfloat16, args.steps, args.warmup, backward=True,
@@ -657,6 +677,7 @@ def main() -> int:
             "launch": "K steps replayed from HIP graphs of up to 10 consecutive steps (graphs of "
                       "one step: secondary.cfg4_one_step_graphs; eager per-call launches: "
                       "secondary.cfg4_eager_launches)",
+            "settle_ms": SETTLE_S * 1e3,
             "parallelism": "single GPU",
         },
         "roofline": roofline,
