@@ -75,15 +75,18 @@ const char* scree_last_error(void);
  * batch + 1 prefix sums rounded up to 16 bytes. */
 size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim);
 
-/* 1 when the attention calls for this problem read the work list
- * scree_attn_schedule writes; 0 when every workgroup derives its own item
- * from cu_seqlens instead (at most 64 sequences and at most 1024 workgroups
- * per launch, i.e. (ceil(total_tokens / 128) + batch) * heads <= 1024: one
- * round of workgroups, where the scheduler launch would be pure latency), so
- * that the schedule call can be skipped.  The workspace argument of the
- * attention calls is still required and size-checked.  No counterpart in the
- * reference. */
-int scree_attn_needs_schedule(int batch, int64_t total_tokens, int heads);
+/* 1 when scree_attn_fwd / scree_attn_fwd_gqa read a work list that
+ * scree_attn_schedule must write first; 0 when the forward derives every
+ * workgroup's item from cu_seqlens itself and leaves the work lists in its
+ * workspace, exactly as scree_attn_schedule writes them, so a forward
+ * followed by backward calls on the same workspace needs no schedule call.
+ * The forward derives for at most 64 sequences in a launch of at most 2048
+ * workgroups at head_dim <= 64, 1024 at head_dim 128, i.e.
+ * (ceil(total_tokens / 128) + batch) * heads within that bound; past it the
+ * derivation (~150 instructions per workgroup) costs more than the scheduler
+ * launch.  Backward calls that no forward on their workspace precedes always
+ * need scree_attn_schedule.  No counterpart in the reference. */
+int scree_attn_needs_schedule(int batch, int64_t total_tokens, int heads, int head_dim);
 
 /* Workspace bytes that let the grouped-query backward split each K/V head's
  * group of query heads over several workgroups (>= scree_attn_workspace_bytes;
@@ -100,11 +103,12 @@ size_t scree_attn_bwd_workspace_bytes_gqa(int batch, int64_t total_tokens, int h
                                           int kv_heads, int head_dim);
 
 /* Build the longest-work-first tile list for `cu_seqlens` into `workspace`.
- * Must precede scree_attn_fwd / scree_attn_bwd with the same cu_seqlens,
- * head_dim and causal flag when scree_attn_needs_schedule returns 1 (calling
- * it anyway is harmless); the workspace may then be reused by any number of
- * forward and backward calls.  No counterpart in the reference (its grid is
- * padded, src/scree/kernels/triton/varlen_attention.py:236). */
+ * Must precede scree_attn_fwd with the same cu_seqlens, head_dim and causal
+ * flag when scree_attn_needs_schedule returns 1, and the backward calls
+ * unless a forward on the same workspace came first (calling it anyway is
+ * harmless); the workspace may then be reused by any number of forward and
+ * backward calls.  No counterpart in the reference (its grid is padded,
+ * src/scree/kernels/triton/varlen_attention.py:236). */
 int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_tokens,
                         int head_dim, int causal, void* workspace, size_t workspace_bytes,
                         void* stream);
@@ -112,12 +116,15 @@ int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_toke
 /* Forward: o = softmax(scale * q k^T [causal-masked]) v per sequence and
  * lse = natural-log logsumexp of the scaled scores per (token, head).
  * strides[8] = {q_row, q_head, k_row, k_head, v_row, v_head, o_row, o_head}.
+ * When scree_attn_needs_schedule returns 0 it derives its work items from
+ * cu_seqlens and writes the work lists into `workspace`; otherwise it reads
+ * the lists scree_attn_schedule wrote there.
  * Replaces _varlen_attn_fwd_kernel + launcher
  * (src/scree/kernels/triton/varlen_attention.py:35-268). */
 int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                    const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
                    int head_dim, const int64_t* strides, float softmax_scale, int causal,
-                   int dtype, const void* workspace, size_t workspace_bytes, void* stream);
+                   int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Backward: dq, dk, dv from dout, the forward's inputs, its output o and lse.
  * delta (total_tokens, heads) fp32 receives rowsum(o * dout).
@@ -160,14 +167,15 @@ int scree_attn_bwd_dkv(const void* dout, const void* q, const void* k, const voi
 int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, float* lse,
                        const int32_t* cu_seqlens, int batch, int64_t total_tokens, int heads,
                        int kv_heads, int head_dim, const int64_t* strides, float softmax_scale,
-                       int causal, int dtype, const void* workspace, size_t workspace_bytes,
+                       int causal, int dtype, void* workspace, size_t workspace_bytes,
                        void* stream);
 
 /* Allocation-free forward.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
- * results as scree_attn_fwd_gqa minus the workspace: the schedule is built
- * on `stream` (as scree_attn_schedule would) into a static device array of
+ * results as scree_attn_fwd_gqa minus the workspace: the work lists are
+ * built on `stream` (by scree_attn_schedule, or by the forward itself when
+ * scree_attn_needs_schedule returns 0) into a static device array of
  * SCREE_ATTN_NOALLOC_SCHEDULE_BYTES per GPU, which holds
  * scree_attn_workspace_bytes() up to that size: 2 * (ceil(total_tokens / 128)
  * + batch) * 16 + 16 bytes (plus the prefix sums past 2048 sequences), i.e.

@@ -397,20 +397,27 @@ __global__ __launch_bounds__(256) void attn_wave_schedule_kernel(const int32_t* 
 }
 
 // ------------------------------------------------- where items come from
-// A launch small enough to run in one round of workgroups (the host decides,
-// attn_derive_items) skips the scheduler launch altogether: every wave of
-// every workgroup derives its own item from cu_seqlens with the code above.
-// That costs each workgroup ~300 instructions before its first load -- a
-// loss when the CUs are full (each workgroup holds its slot longer) but far
-// less than the scheduler launch (~3.5 us of dependent latency) when the
-// launch is latency-bound.  Larger launches read the scheduler's list.
+// The forward of a batch of at most kWaveSched sequences in a launch of a few
+// rounds of workgroups (attn_fwd_derives) needs no scheduler launch: every
+// wave of every workgroup derives its own item from cu_seqlens with the code
+// above (~150 instructions before its first load), and the forward leaves
+// the header and its work-order list in the workspace exactly as
+// attn_wave_schedule_kernel writes them (the last block the header; the
+// head-0 workgroup of each item that item's entry), so the backward passes that
+// follow read them.  Such a launch is head-minor, and so are both backward
+// passes of the problem (the dQ grid is the forward's, the dK/dV grid at most
+// that): none reads the sequence-major list, which stays as it was.  The
+// backward passes always read the lists: deriving there cost more (dQ +1.9,
+// dK/dV +1.5 us at config 4) than the forward does (+1.0 us), and the
+// forward saves the scheduler launch (3.4 us).
 struct ItemSource {
   const int32_t* header;
   const int4* items;  // the list this launch reads
   const int32_t* cu;
+  int32_t* publish;   // workspace the deriving forward writes the lists into
   int batch, total_tokens;
   int seq_major;      // the sequence-major list (head-major launches)
-  int derive;         // derive items from cu (batch <= kWaveSched)
+  int derive;         // derive items from cu (the forward, batch <= kWaveSched)
 };
 
 // The schedule as this wave sees it: whether it failed (offsets that
@@ -418,25 +425,47 @@ struct ItemSource {
 // listed item are loaded in both modes (the workspace always holds them;
 // stale bytes when deriving) so that on the list path their loads issue
 // with the kernel arguments rather than after a branch on src.derive.
+// MAY_DERIVE false (the backward passes) compiles the list path alone.
 struct ItemView {
   WaveSched w;
   bool failed;
   int count;
 };
+template <bool MAY_DERIVE>
 __device__ __forceinline__ ItemView item_view(const ItemSource& src, int tmax) {
   const int listed_count = src.header[0], listed_batch = src.header[1];
   ItemView v;
   v.w = WaveSched{0, 0, 0, 0, 0};
-  if (src.derive) v.w = wave_sched(src.cu, src.batch, src.total_tokens);
-  v.failed = src.derive ? v.w.total > tmax : listed_batch < 0;
-  v.count = src.derive ? (v.failed ? 0 : v.w.total) : listed_count;
+  if (MAY_DERIVE && src.derive) v.w = wave_sched(src.cu, src.batch, src.total_tokens);
+  const bool derive = MAY_DERIVE && src.derive;
+  v.failed = derive ? v.w.total > tmax : listed_batch < 0;
+  v.count = derive ? (v.failed ? 0 : v.w.total) : listed_count;
   return v;
 }
+template <bool MAY_DERIVE>
 __device__ __forceinline__ int4 item_at(const ItemSource& src, const ItemView& v, bool causal, int p) {
   const int4 listed = src.items[p];
   int4 it = make_int4(0, 0, 0, 0);
-  if (src.derive) it = wave_item(v.w, src.batch, causal, src.seq_major != 0, p);
-  return src.derive ? it : listed;
+  if (MAY_DERIVE && src.derive) it = wave_item(v.w, src.batch, causal, src.seq_major != 0, p);
+  return MAY_DERIVE && src.derive ? it : listed;
+}
+
+// The deriving forward's share of the schedule: the last block (the
+// shortest item, or none; block 0 runs the longest) writes the header
+// (failed offsets: no items and batch -1, as the scheduler publishes them),
+// on whichever path it leaves the kernel.
+__device__ __forceinline__ void publish_header(const ItemSource& src, const ItemView& v, int causal) {
+  if (src.publish && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
+    src.publish[0] = v.count;
+    src.publish[1] = v.failed ? -1 : src.batch;
+    src.publish[2] = kBM;
+    src.publish[3] = causal;
+  }
+}
+// Item p of the work-order list, from the head-0 workgroup of item p.
+__device__ __forceinline__ void publish_item(const ItemSource& src, int p, const int4& it) {
+  if (src.publish && threadIdx.x == 0)
+    reinterpret_cast<int4*>(src.publish + kHeaderBytes / sizeof(int32_t))[p] = it;
 }
 
 // ------------------------------------------------- batches past kMaxBatch
@@ -1005,16 +1034,20 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
   __shared__ __align__(16) T smem[2 * BUF];
   static_assert(4 * stage_elems<D>() <= 2 * BUF, "O staging must fit in the tile buffers");
 
-  const ItemView iv = item_view(src, tmax);
+  const ItemView iv = item_view<true>(src, tmax);
   if (iv.failed) {
+    publish_header(src, iv, CAUSAL ? 1 : 0);
     poison_rows(o, so, total, heads, D);
     poison_stats(lse, total, heads);
     return;
   }
   int item, h;
-  if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) return;
+  if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) {
+    publish_header(src, iv, CAUSAL ? 1 : 0);
+    return;
+  }
   const int hk = h / group;  // K/V head of this query head
-  const int4 it = item_at(src, iv, CAUSAL, item);
+  const int4 it = item_at<true>(src, iv, CAUSAL, item);
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   FwdState<T, D> st;
   st.wave = wave_id();
@@ -1092,6 +1125,9 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
     if (st.g == 0 && my_q < L)
       lse[(int64_t)(start + my_q) * heads + h] = st.m_run * scale + logf(l_tot);
   }
+  // last: a store issued earlier would hold up the prologue's counter waits
+  publish_header(src, iv, CAUSAL ? 1 : 0);
+  if (h == 0) publish_item(src, item, it);
 }
 
 // ------------------------------------------- dQ pass: folded score scale
@@ -1263,7 +1299,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   __shared__ __align__(16) T smem[dq_nbuf<D>() * BUF];
   static_assert(4 * stage_elems<D>() <= dq_nbuf<D>() * BUF, "dQ staging must fit in the tile buffers");
 
-  const ItemView iv = item_view(src, tmax);
+  const ItemView iv = item_view<false>(src, tmax);
   if (iv.failed) {
     poison_rows(dq, sdq, total, heads, D);
     poison_stats(delta, total, heads);
@@ -1272,7 +1308,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   int item, h;
   if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) return;
   const int hk = h / group;  // K/V head of this query head
-  const int4 it = item_at(src, iv, CAUSAL, item);
+  const int4 it = item_at<false>(src, iv, CAUSAL, item);
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   DqState<T, D> st;
   st.wave = wave_id();
@@ -1538,9 +1574,9 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(
   constexpr int CHUNKS = kBM / kRedRows;
   const int slot = blockIdx.x / CHUNKS, chunk = blockIdx.x % CHUNKS;
   const int item = slot / kv_heads, hk = slot % kv_heads;
-  const ItemView iv = item_view(src, tmax);  // a failed schedule: the pass poisoned dk / dv
+  const ItemView iv = item_view<false>(src, tmax);  // a failed schedule: the pass poisoned dk / dv
   if (item >= iv.count) return;
-  const int4 it = item_at(src, iv, causal != 0, item);
+  const int4 it = item_at<false>(src, iv, causal != 0, item);
   const int start = it.z, L = it.w;
   const int k0 = ((L + kBM - 1) / kBM - 1 - it.y) * kBM;
   constexpr int C4 = D / 4;
@@ -1600,7 +1636,7 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   // and their contributions accumulate in the dK / dV registers.  With
   // gsplit > 1 parts, each part stores its fp32 sums and dkv_reduce_kernel
   // adds them up after the pass.
-  const ItemView iv = item_view(src, tmax);
+  const ItemView iv = item_view<false>(src, tmax);
   if (iv.failed) {
     poison_rows(dk, sdk, total, kv_heads, D);
     poison_rows(dv, sdv, total, kv_heads, D);
@@ -1611,7 +1647,7 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   const int hk = hv % kv_heads, part = hv / kv_heads;
   const int g0 = part * group / gsplit, g1 = (part + 1) * group / gsplit;
   const int heads = kv_heads * group;
-  const int4 it = item_at(src, iv, CAUSAL, item);
+  const int4 it = item_at<false>(src, iv, CAUSAL, item);
   const int start = it.z, L = it.w;
   const int nblk = (L + kBM - 1) / kBM;
   const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
@@ -1802,29 +1838,40 @@ inline const int4* schedule_list(const void* ws, int tmax, int head_major) {
   return reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes) +
          (head_major ? tmax : 0);
 }
-// Launches of at most one round of workgroups (256 CUs x 4) over at most
-// kWaveSched sequences derive their items in the kernels (see ItemSource);
-// the decision depends only on the batch, the token count and the query
-// heads, so every pass of one problem takes the same one.
-constexpr int64_t kDeriveMaxBlocks = 1024;
-inline bool attn_derive_items(int batch, int64_t tmax, int heads) {
-  return batch <= kWaveSched && tmax * heads <= kDeriveMaxBlocks;
+// The forward derives its items (and publishes the lists) for batches of at
+// most kWaveSched sequences in launches of a few rounds of workgroups; the
+// backward passes read the lists.  Deriving costs each round of workgroups
+// ~0.6 us at head_dim <= 64 (four or three workgroups per CU) and ~1.2 us at
+// 128 (two): config 4's 1,776 workgroups pay +1.0 us against the scheduler's
+// 3.4, config 5's 23,040 at head_dim 128 +55 us.
+constexpr int64_t kFwdDeriveMaxBlocks = 2048;  // 1024 at head_dim 128
+static_assert(kFwdDeriveMaxBlocks < (int64_t)kXcds * 512,
+              "a deriving forward's problem must have no head-major pass (attn_head_major)");
+inline bool attn_fwd_derives(int batch, int64_t tmax, int heads, int head_dim) {
+  return batch <= kWaveSched &&
+         tmax * heads <= (head_dim <= 64 ? kFwdDeriveMaxBlocks : kFwdDeriveMaxBlocks / 2);
 }
-inline ItemSource item_source(const void* ws, const int32_t* cu, int batch, int total, int tmax,
-                              int head_major, int heads) {
-  return ItemSource{static_cast<const int32_t*>(ws), schedule_list(ws, tmax, head_major), cu, batch,
-                    total, head_major, attn_derive_items(batch, tmax, heads) ? 1 : 0};
+inline ItemSource fwd_item_source(void* ws, const int32_t* cu, int batch, int total, int tmax,
+                                  int heads, int head_dim, int head_major) {
+  const bool derive = attn_fwd_derives(batch, tmax, heads, head_dim);
+  return ItemSource{static_cast<const int32_t*>(ws), schedule_list(ws, tmax, head_major), cu,
+                    derive ? static_cast<int32_t*>(ws) : nullptr, batch, total, head_major,
+                    derive ? 1 : 0};
+}
+inline ItemSource list_item_source(const void* ws, int tmax, int head_major) {
+  return ItemSource{static_cast<const int32_t*>(ws), schedule_list(ws, tmax, head_major), nullptr,
+                    nullptr, 0, 0, head_major, 0};
 }
 
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
                   const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
-                  float scale, int tmax, const void* ws, int total, hipStream_t stream) {
+                  float scale, int tmax, void* ws, int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int hm = attn_head_major(heads, tmax);
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(o), lse, item_source(ws, cu, batch, total, tmax, hm, heads),
+                     static_cast<T*>(o), lse, fwd_item_source(ws, cu, batch, total, tmax, heads, D, hm),
                      tmax, hm,
                      heads, heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
                      Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e, total);
@@ -1842,7 +1889,7 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<const T*>(o), lse, delta, static_cast<T*>(dq),
-                     item_source(ws, cu, batch, total, tmax, hm, heads), tmax, hm, heads,
+                     list_item_source(ws, tmax, hm), tmax, hm, heads,
                      heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
@@ -1858,7 +1905,7 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
   // one workgroup per (item, K/V head, part of the head group)
   const int64_t grid = (int64_t)tmax * kv_heads * gsplit;
   const int hm = attn_head_major(kv_heads * gsplit, tmax);
-  const ItemSource src = item_source(ws, cu, batch, total, tmax, hm, heads);
+  const ItemSource src = list_item_source(ws, tmax, hm);
   // the split epilogue has a kernel of its own: its registers would cost the
   // unsplit kernel a wave per SIMD at D = 64
   // (a split group never has the many rounds of a head-major launch)
@@ -1898,9 +1945,10 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
 
 using namespace scree;
 
-extern "C" int scree_attn_needs_schedule(int batch, int64_t total_tokens, int heads) {
+extern "C" int scree_attn_needs_schedule(int batch, int64_t total_tokens, int heads,
+                                         int head_dim) {
   if (batch < 1 || total_tokens < 0 || heads < 1) return 1;
-  return attn_derive_items(batch, tmax_for(batch, total_tokens), heads) ? 0 : 1;
+  return attn_fwd_derives(batch, tmax_for(batch, total_tokens), heads, head_dim) ? 0 : 1;
 }
 
 extern "C" size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim) {
@@ -1987,7 +2035,7 @@ static int check_fwd(const char* fn, const void* q, const void* k, const void* v
 static int launch_fwd(const char* fn, const void* q, const void* k, const void* v, void* o,
                       float* lse, const int32_t* cu_seqlens, int batch, int64_t total_tokens,
                       int heads, int kv_heads, int head_dim, const int64_t* strides,
-                      float softmax_scale, int causal, int dtype, const void* workspace,
+                      float softmax_scale, int causal, int dtype, void* workspace,
                       void* stream) {
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
@@ -2001,7 +2049,7 @@ extern "C" int scree_attn_fwd_gqa(const void* q, const void* k, const void* v, v
                                   float* lse, const int32_t* cu_seqlens, int batch,
                                   int64_t total_tokens, int heads, int kv_heads, int head_dim,
                                   const int64_t* strides, float softmax_scale, int causal,
-                                  int dtype, const void* workspace, size_t workspace_bytes,
+                                  int dtype, void* workspace, size_t workspace_bytes,
                                   void* stream) {
   const char* fn = "scree_attn_fwd";
   int rc = check_fwd(fn, q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, kv_heads,
@@ -2069,7 +2117,7 @@ extern "C" int scree_attn_fwd_noalloc(const void* q, const void* k, const void* 
   if (rc) return rc;
   if (total_tokens == 0) return SCREE_OK;
   if ((rc = scratch_for_current_device(fn, &ws))) return rc;
-  if (scree_attn_needs_schedule(batch, total_tokens, heads)) {
+  if (scree_attn_needs_schedule(batch, total_tokens, heads, head_dim)) {
     rc = scree_attn_schedule(cu_seqlens, batch, total_tokens, head_dim, causal, ws,
                              SCREE_ATTN_NOALLOC_SCHEDULE_BYTES, stream);
     if (rc) return rc;
@@ -2081,7 +2129,7 @@ extern "C" int scree_attn_fwd_noalloc(const void* q, const void* k, const void* 
 extern "C" int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                               const int32_t* cu_seqlens, int batch, int64_t total_tokens,
                               int heads, int head_dim, const int64_t* strides, float softmax_scale,
-                              int causal, int dtype, const void* workspace,
+                              int causal, int dtype, void* workspace,
                               size_t workspace_bytes, void* stream) {
   return scree_attn_fwd_gqa(q, k, v, o, lse, cu_seqlens, batch, total_tokens, heads, heads,
                             head_dim, strides, softmax_scale, causal, dtype, workspace,

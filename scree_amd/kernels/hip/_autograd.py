@@ -5,10 +5,11 @@ Mirrors ``varlen_attention_triton_autograd``
 ``(q, k, v, out, lse, cu_seqlens)`` and backward returns ``(dq, dk, dv, None,
 None)``.  Two differences: the Function class is defined once at import
 (the reference rebuilds it on every call, ``_autograd.py:71``), and the
-forward also keeps the device work list it built (schedule-sized: 16 bytes
-per 128-token block plus 16 per sequence; small launches need no list, their
-workgroups derive their items from the offsets), so the backward launches no
-scheduler and never synchronises the host.  When the grouped-query dK/dV
+forward also keeps its workspace, which holds the device work lists
+(schedule-sized: 16 bytes per 128-token block plus 16 per sequence; built by
+the scheduler past 64 sequences, else by the forward kernel itself as it
+derives its items from the offsets), so the backward launches no scheduler
+and never synchronises the host.  When the grouped-query dK/dV
 split pays, the backward allocates the larger workspace it needs for the
 duration of the pass and copies the work list into it on the device.
 """

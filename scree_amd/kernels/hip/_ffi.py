@@ -33,7 +33,7 @@ _S = ctypes.c_size_t
 _SIGNATURES = {
     "scree_abi_version": (_I, []),
     "scree_last_error": (ctypes.c_char_p, []),
-    "scree_attn_needs_schedule": (_I, [_I, _L, _I]),
+    "scree_attn_needs_schedule": (_I, [_I, _L, _I, _I]),
     "scree_attn_workspace_bytes": (_S, [_I, _L, _I]),
     "scree_attn_bwd_workspace_bytes_gqa": (_S, [_I, _L, _I, _I, _I]),
     "scree_attn_schedule": (_I, [_P, _I, _L, _I, _I, _P, _S, _P]),

@@ -82,21 +82,24 @@ def workspace_bytes(batch: int, total: int, head_dim: int) -> int:
     return int(_ffi.lib().scree_attn_workspace_bytes(batch, total, head_dim))
 
 
-def needs_schedule(batch: int, total: int, heads: int) -> bool:
-    """Whether the kernels read the work list of :func:`attention_schedule`.
-    Small launches (at most 64 sequences and one round of workgroups) derive
-    their items from ``cu_seqlens`` inside every workgroup instead, which
-    saves the scheduler launch's latency."""
-    return bool(_ffi.lib().scree_attn_needs_schedule(batch, total, heads))
+def needs_schedule(batch: int, total: int, heads: int, head_dim: int) -> bool:
+    """Whether the forward reads a work list that :func:`attention_schedule`
+    must build first.  At most 64 sequences in a launch of a few rounds of
+    workgroups need none: the forward derives its items from ``cu_seqlens``
+    and leaves the lists in its workspace for the backward calls that follow
+    on the same workspace."""
+    return bool(_ffi.lib().scree_attn_needs_schedule(batch, total, heads, head_dim))
 
 
 def prepare_workspace(cu_seqlens: torch.Tensor, total_tokens: int, head_dim: int, causal: bool,
-                      heads: int, workspace: torch.Tensor = None) -> torch.Tensor:
-    """A workspace the attention calls accept for these offsets and heads:
-    the work list built into it when the launches read one, else the room
-    alone (allocated when ``workspace`` is None)."""
+                      heads: int, workspace: torch.Tensor = None,
+                      for_backward: bool = False) -> torch.Tensor:
+    """A workspace for the attention calls on these offsets: the work lists
+    built into it when the forward reads them, or when ``for_backward`` (a
+    backward that no forward on this workspace precedes), else the room alone
+    (allocated when ``workspace`` is None), which the forward fills."""
     batch = cu_seqlens.numel() - 1
-    if needs_schedule(batch, total_tokens, heads):
+    if for_backward or needs_schedule(batch, total_tokens, heads, head_dim):
         return attention_schedule(cu_seqlens, total_tokens, head_dim, causal, workspace)
     if workspace is None:
         workspace = torch.empty(workspace_bytes(batch, total_tokens, head_dim), dtype=torch.uint8,
@@ -272,6 +275,7 @@ def varlen_attention_hip_backward(do, q, k, v, o, lse, cu_seqlens, causal: bool 
     with torch.cuda.device(q.device):
         if workspace is None:
             workspace = prepare_workspace(cu, total, head_dim, causal, n_heads,
-                                          _bwd_workspace(cu, total, n_heads, k.shape[1], head_dim))
+                                          _bwd_workspace(cu, total, n_heads, k.shape[1], head_dim),
+                                          for_backward=True)
         _attn_bwd(*ins, lse.contiguous(), cu, causal, dq, dk, dv, delta, workspace)
     return dq, dk, dv

@@ -72,14 +72,19 @@ def test_workspace_sizes():
     # header + two lists of (ceil(N/128) + B) int4 items
     assert lib.scree_attn_workspace_bytes(16, 12160, 64) == 16 + 2 * 16 * (95 + 16)
     assert lib.scree_attn_workspace_bytes(0, 10, 64) == 0
-    # launches of one round of workgroups ((ceil(N/128) + B) * heads <= 1024)
-    # over at most 64 sequences derive their items: no schedule needed
-    assert lib.scree_attn_needs_schedule(16, 1980, 4) == 0      # config 1: 32 x 4 workgroups
-    assert lib.scree_attn_needs_schedule(16, 12160, 16) == 1    # config 4: 111 x 16
-    assert lib.scree_attn_needs_schedule(64, 1024, 1) == 0
-    assert lib.scree_attn_needs_schedule(65, 1024, 1) == 1      # past one wavefront of sequences
-    assert lib.scree_attn_needs_schedule(16, 12160, 9) == 0     # 111 x 9 = 999
-    assert lib.scree_attn_needs_schedule(16, 12160, 10) == 1    # 1110
+    # a forward over at most 64 sequences (one wavefront) in a launch of at
+    # most 2048 workgroups (1024 at head_dim 128), (ceil(N/128) + B) * heads,
+    # derives its items and writes the lists itself: no schedule needed
+    assert lib.scree_attn_needs_schedule(16, 1980, 4, 32) == 0      # config 1: 32 x 4
+    assert lib.scree_attn_needs_schedule(16, 12160, 16, 64) == 0    # config 4: 111 x 16
+    assert lib.scree_attn_needs_schedule(32, 83977, 32, 128) == 1   # config 5: 689 x 32
+    assert lib.scree_attn_needs_schedule(16, 12160, 18, 64) == 0    # 111 x 18 = 1998
+    assert lib.scree_attn_needs_schedule(16, 12160, 19, 64) == 1    # 2109
+    assert lib.scree_attn_needs_schedule(16, 12160, 9, 128) == 0    # 999
+    assert lib.scree_attn_needs_schedule(16, 12160, 10, 128) == 1   # 1110
+    assert lib.scree_attn_needs_schedule(64, 1024, 1, 64) == 0
+    assert lib.scree_attn_needs_schedule(65, 1024, 1, 64) == 1      # past one wavefront of sequences
+    assert lib.scree_attn_needs_schedule(0, 10, 4, 64) == 1         # invalid: the call will say why
     # past 2048 sequences the (natural-order) scheduler keeps batch + 1
     # prefix sums after the lists, rounded up to 16 bytes
     lists = 16 + 2 * 16 * (24 + 3000)

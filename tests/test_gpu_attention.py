@@ -189,55 +189,71 @@ def test_batch_past_the_sorting_scheduler(causal):
     _run_case(lengths, 2, 64, torch.float16, causal, seed=25)
 
 
-def test_small_launch_reads_no_work_list():
-    """A launch small enough to derive its items from the offsets gives the
-    same outputs, bit for bit, with a workspace of stale bytes."""
-    from scree_amd.kernels.hip import (needs_schedule, varlen_attention_hip,
-                                       varlen_attention_hip_backward)
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_publishes_the_schedule(causal):
+    """A forward that needs no schedule derives its items and leaves in a
+    workspace of stale bytes the header and the work-order list, bit for bit
+    as the scheduler writes them (which the oracle pins): grouped-query head
+    order, head_dim 128, empty sequences, one sequence, a full wave of 64,
+    the largest launch that derives.  (The sequence-major list serves only
+    head-major passes, which no problem small enough to derive has.)"""
+    from scree_amd.kernels.hip import attention as A
+    from scree_amd.kernels.hip import attention_schedule, needs_schedule, schedule_items
+
+    rng = np.random.default_rng(31)
+    c4 = workloads.config4().lengths
+    cases = [  # (lengths, heads, kv_heads, head_dim)
+        ([300, 17, 129, 640, 1, 0, 77], 4, 4, 64),
+        ([300, 17, 129, 640, 1, 0, 77], 8, 8, 128),
+        ([5], 2, 2, 32),
+        (c4, 16, 16, 64),
+        (c4, 18, 18, 64),                      # 1,998 workgroups: the largest that derive
+        (c4, 16, 4, 64),                       # grouped-query head permutation
+        ([int(x) for x in rng.integers(0, 400, size=64)], 2, 2, 32),
+    ]
+    for lengths, heads, kvh, d in cases:
+        n, b = int(sum(lengths)), len(lengths)
+        say(f"case: published schedule B={b} N={n} H={heads}/{kvh} D={d} causal={causal}")
+        assert not needs_schedule(b, n, heads, d)
+        off, cu = cu_of(lengths)
+        q = randn((n, heads, d), torch.float16, 70)
+        k, v = (randn((n, kvh, d), torch.float16, 71 + i) for i in range(2))
+        stale = torch.full((A.workspace_bytes(b, n, d),), 255, dtype=torch.uint8, device="cuda")
+        out = torch.empty_like(q)
+        lse = torch.empty((n, heads), dtype=torch.float32, device="cuda")
+        A._attn_fwd(q, k, v, cu, causal, out, lse, stale)
+        want = attention_schedule(cu, n, d, causal)
+        torch.cuda.synchronize()
+        assert stale[:16].view(torch.int32).tolist() == want[:16].view(torch.int32).tolist()
+        cw, iw = schedule_items(want, with_ranges=True)
+        cg, ig = schedule_items(stale, with_ranges=True)
+        assert cg == cw
+        np.testing.assert_array_equal(ig.numpy(), iw.numpy())
+
+
+def test_backward_reads_the_forwards_lists():
+    """Forward then backward on one workspace of stale bytes, no schedule
+    call: the same outputs and gradients, bit for bit, as the standalone
+    backward, which schedules its own workspace."""
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
     from scree_amd.kernels.hip import attention as A
 
-    lengths = [300, 17, 129, 640, 1, 0, 77]
-    n = sum(lengths)
-    say(f"case: stale workspace B={len(lengths)} N={n} H=4")
-    assert not needs_schedule(len(lengths), n, 4)
-    off, cu = cu_of(lengths)
-    q, k, v, do = (randn((n, 4, 64), torch.float16, 50 + i) for i in range(4))
-    ref = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
-    ref_g = varlen_attention_hip_backward(do, q, k, v, ref[0], ref[1], cu, causal=True)
-    stale = torch.full((A.workspace_bytes(len(lengths), n, 64),), 255, dtype=torch.uint8,
-                       device="cuda")
-    got = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True, workspace=stale)
-    got_g = varlen_attention_hip_backward(do, q, k, v, got[0], got[1], cu, causal=True,
-                                          workspace=stale)
-    torch.cuda.synchronize()
-    assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
-    for a, b in zip(ref_g, got_g):
-        assert torch.equal(a, b)
-
-
-@pytest.mark.parametrize("causal", [True, False])
-def test_derived_and_listed_items_agree(causal):
-    """Heads are independent: config 4's lengths at 16 heads (1,776
-    workgroups, read from the scheduler's list) and the first 4 of those heads
-    alone (444 workgroups, items derived in the kernels) give the same
-    outputs and gradients for those heads, bit for bit."""
-    from scree_amd.kernels.hip import needs_schedule, varlen_attention_hip, varlen_attention_hip_backward
-
-    c = workloads.config4()
-    n = sum(c.lengths)
-    say(f"case: derived vs listed items, config 4 lengths, causal={causal}")
-    assert needs_schedule(len(c.lengths), n, 16) and not needs_schedule(len(c.lengths), n, 4)
-    off, cu = cu_of(c.lengths)
-    q, k, v, do = (randn((n, 16, 64), torch.float16, 60 + i) for i in range(4))
-    o16, l16 = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True)
-    g16 = varlen_attention_hip_backward(do, q, k, v, o16, l16, cu, causal=causal)
-    sub = [t[:, :4].contiguous() for t in (q, k, v, do)]
-    o4, l4 = varlen_attention_hip(*sub[:3], cu, causal=causal, return_lse=True)
-    g4 = varlen_attention_hip_backward(sub[3], *sub[:3], o4, l4, cu, causal=causal)
-    torch.cuda.synchronize()
-    assert torch.equal(o16[:, :4], o4) and torch.equal(l16[:, :4], l4)
-    for a, b in zip(g16, g4):
-        assert torch.equal(a[:, :4], b)
+    for lengths, heads in (([300, 17, 129, 640, 1, 0, 77], 4), (workloads.config4().lengths, 16)):
+        n = sum(lengths)
+        say(f"case: forward-built lists B={len(lengths)} N={n} H={heads}")
+        off, cu = cu_of(lengths)
+        q, k, v, do = (randn((n, heads, 64), torch.float16, 50 + i) for i in range(4))
+        ref = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+        ref_g = varlen_attention_hip_backward(do, q, k, v, ref[0], ref[1], cu, causal=True)
+        stale = torch.full((A.workspace_bytes(len(lengths), n, 64),), 255, dtype=torch.uint8,
+                           device="cuda")
+        got = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True, workspace=stale)
+        got_g = varlen_attention_hip_backward(do, q, k, v, got[0], got[1], cu, causal=True,
+                                              workspace=stale)
+        torch.cuda.synchronize()
+        assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
+        for a, b in zip(ref_g, got_g):
+            assert torch.equal(a, b)
 
 
 def test_config3_fixed_list_fp16_causal():
