@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import torch
 
+from . import _ffi
 from . import attention as _attn
 
 
@@ -30,7 +31,7 @@ class VarlenAttentionHip(torch.autograd.Function):
         qk, kk, vk = _attn._kernel_view(q), _attn._kernel_view(k), _attn._kernel_view(v)
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         lse = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
-        with torch.cuda.device(q.device):
+        with _ffi.device_guard(q.device):
             ws = _attn.prepare_workspace(cu, total, head_dim, causal, n_heads)
             _attn._attn_fwd(qk, kk, vk, cu, causal, out, lse, ws)
         ctx.save_for_backward(qk, kk, vk, out, lse, cu, ws)
@@ -46,7 +47,7 @@ class VarlenAttentionHip(torch.autograd.Function):
         dv = torch.empty_like(v, memory_format=torch.contiguous_format)
         total, n_heads, _ = q.shape
         delta = torch.empty((total, n_heads), dtype=torch.float32, device=q.device)
-        with torch.cuda.device(q.device):
+        with _ffi.device_guard(q.device):
             need = _attn.bwd_workspace_bytes(cu.numel() - 1, total, n_heads, k.shape[1], q.shape[2])
             if need > ws.numel():  # grouped-query split: work list + fp32 partials
                 big = torch.empty(need, dtype=torch.uint8, device=q.device)

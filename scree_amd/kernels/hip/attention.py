@@ -26,6 +26,7 @@ Differences a caller can observe:
 
 from __future__ import annotations
 
+import functools
 import math
 
 import torch
@@ -57,14 +58,15 @@ def _kernel_view(t: torch.Tensor) -> torch.Tensor:
     multiples of 8 elements below 2^24, a 16-byte aligned base, and rows that
     do not overlap -- exactly what ``check_tensor`` in the library accepts.
     """
+    s0, s1, s2 = t.stride()
     ok = (
-        t.stride(2) == 1
-        and t.stride(0) % 8 == 0
-        and t.stride(1) % 8 == 0
-        and 0 <= t.stride(0) < _MAX_STRIDE
-        and 0 <= t.stride(1) < _MAX_STRIDE
+        s2 == 1
+        and s0 % 8 == 0
+        and s1 % 8 == 0
+        and 0 <= s0 < _MAX_STRIDE
+        and 0 <= s1 < _MAX_STRIDE
         and t.data_ptr() % 16 == 0
-        and (t.shape[0] <= 1 or t.stride(0) >= t.shape[2])
+        and (t.shape[0] <= 1 or s0 >= t.shape[2])
     )
     return t if ok else t.contiguous()
 
@@ -78,10 +80,14 @@ def _cu(cu_seqlens: torch.Tensor, device) -> torch.Tensor:
     return cu.contiguous()
 
 
+# The size and mode queries are pure functions of a few integers; a training
+# loop asks them with the same arguments every step.
+@functools.lru_cache(maxsize=256)
 def workspace_bytes(batch: int, total: int, head_dim: int) -> int:
     return int(_ffi.lib().scree_attn_workspace_bytes(batch, total, head_dim))
 
 
+@functools.lru_cache(maxsize=256)
 def needs_schedule(batch: int, total: int, heads: int, head_dim: int) -> bool:
     """Whether the forward reads a work list that :func:`attention_schedule`
     must build first.  At most 64 sequences in a launch of a few rounds of
@@ -107,6 +113,7 @@ def prepare_workspace(cu_seqlens: torch.Tensor, total_tokens: int, head_dim: int
     return workspace
 
 
+@functools.lru_cache(maxsize=256)
 def bwd_workspace_bytes(batch: int, total: int, heads: int, kv_heads: int, head_dim: int) -> int:
     """Workspace bytes for a forward + backward with ``kv_heads`` K/V heads:
     the schedule, plus room for the grouped-query dK/dV split when it pays."""
@@ -131,7 +138,7 @@ def attention_schedule(cu_seqlens: torch.Tensor, total_tokens: int, head_dim: in
     nbytes = workspace_bytes(batch, total_tokens, head_dim)
     if workspace is None:
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=cu_seqlens.device)
-    with torch.cuda.device(cu_seqlens.device):
+    with _ffi.device_guard(cu_seqlens.device):
         _ffi.check(lib.scree_attn_schedule(
             _ffi.ptr(cu_seqlens), batch, total_tokens, head_dim, int(bool(causal)),
             _ffi.ptr(workspace), workspace.numel(), _ffi.stream_of(cu_seqlens)))
@@ -157,8 +164,7 @@ def schedule_items(workspace: torch.Tensor, with_ranges: bool = False, by_sequen
 def _attn_fwd(q, k, v, cu, causal, out, lse, workspace):
     lib = _ffi.lib()
     total, heads, head_dim = q.shape
-    strides = _ffi.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1),
-                                v.stride(0), v.stride(1), out.stride(0), out.stride(1)])
+    strides = _ffi.int64_array(q.stride()[:2] + k.stride()[:2] + v.stride()[:2] + out.stride()[:2])
     _ffi.check(lib.scree_attn_fwd_gqa(
         _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(out), _ffi.ptr(lse), _ffi.ptr(cu),
         cu.numel() - 1, total, heads, k.shape[1], head_dim, strides, 1.0 / math.sqrt(head_dim),
@@ -170,7 +176,7 @@ def _attn_bwd(do, q, k, v, o, lse, cu, causal, dq, dk, dv, delta, workspace):
     lib = _ffi.lib()
     total, heads, head_dim = q.shape
     ts = (do, q, k, v, o, dq, dk, dv)
-    strides = _ffi.int64_array([s for t in ts for s in (t.stride(0), t.stride(1))])
+    strides = _ffi.int64_array(sum((t.stride()[:2] for t in ts), ()))
     _ffi.check(lib.scree_attn_bwd_gqa(
         _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(o), _ffi.ptr(lse),
         _ffi.ptr(dq), _ffi.ptr(dk), _ffi.ptr(dv), _ffi.ptr(delta), _ffi.ptr(cu),
@@ -182,7 +188,7 @@ def _attn_bwd(do, q, k, v, o, lse, cu, causal, dq, dk, dv, delta, workspace):
 def _attn_bwd_dq(do, q, k, v, o, lse, cu, causal, dq, delta, workspace):
     lib = _ffi.lib()
     total, heads, head_dim = q.shape
-    strides = _ffi.int64_array([s for t in (do, q, k, v, o, dq) for s in (t.stride(0), t.stride(1))])
+    strides = _ffi.int64_array(sum((t.stride()[:2] for t in (do, q, k, v, o, dq)), ()))
     _ffi.check(lib.scree_attn_bwd_dq_gqa(
         _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(o), _ffi.ptr(lse),
         _ffi.ptr(dq), _ffi.ptr(delta), _ffi.ptr(cu), cu.numel() - 1, total, heads, k.shape[1],
@@ -193,7 +199,7 @@ def _attn_bwd_dq(do, q, k, v, o, lse, cu, causal, dq, delta, workspace):
 def _attn_bwd_dkv(do, q, k, v, lse, delta, cu, causal, dk, dv, workspace):
     lib = _ffi.lib()
     total, heads, head_dim = q.shape
-    strides = _ffi.int64_array([s for t in (do, q, k, v, dk, dv) for s in (t.stride(0), t.stride(1))])
+    strides = _ffi.int64_array(sum((t.stride()[:2] for t in (do, q, k, v, dk, dv)), ()))
     _ffi.check(lib.scree_attn_bwd_dkv_gqa(
         _ffi.ptr(do), _ffi.ptr(q), _ffi.ptr(k), _ffi.ptr(v), _ffi.ptr(lse), _ffi.ptr(delta),
         _ffi.ptr(dk), _ffi.ptr(dv), _ffi.ptr(cu), cu.numel() - 1, total, heads, k.shape[1],
@@ -233,7 +239,7 @@ def varlen_attention_hip(q, k, v, cu_seqlens, causal: bool = False, block_m: int
     cu = _cu(cu_seqlens, q.device)
     qk, kk, vk = _kernel_view(q), _kernel_view(k), _kernel_view(v)
     ok = _kernel_view(out)
-    with torch.cuda.device(q.device):
+    with _ffi.device_guard(q.device):
         if workspace is None:
             workspace = prepare_workspace(cu, total, head_dim, causal, n_heads)
         _attn_fwd(qk, kk, vk, cu, causal, ok, lse, workspace)
@@ -272,7 +278,7 @@ def varlen_attention_hip_backward(do, q, k, v, o, lse, cu_seqlens, causal: bool 
         assert delta_buffer.is_contiguous(), "delta_buffer must be contiguous"
         delta = delta_buffer
     ins = [_kernel_view(t) for t in (do, q, k, v, o)]
-    with torch.cuda.device(q.device):
+    with _ffi.device_guard(q.device):
         if workspace is None:
             workspace = prepare_workspace(cu, total, head_dim, causal, n_heads,
                                           _bwd_workspace(cu, total, n_heads, k.shape[1], head_dim),

@@ -48,7 +48,7 @@ def rmsnorm_fwd(x2, w, eps, want_stats):
     rows, d = x2.shape
     y = torch.empty_like(x2)
     rstd = torch.empty(rows, dtype=torch.float32, device=x2.device) if want_stats else None
-    with torch.cuda.device(x2.device):
+    with _ffi.device_guard(x2.device):
         _ffi.check(_ffi.lib().scree_rmsnorm_fwd(
             _ffi.ptr(x2), _ffi.ptr(w), _ffi.ptr(y), _ffi.ptr(rstd), rows, d, float(eps),
             _ffi.dtype_code(x2.dtype), _ffi.stream_of(x2)))
@@ -62,7 +62,7 @@ def layernorm_fwd(x2, w, b, eps, want_stats):
     if want_stats:
         mean = torch.empty(rows, dtype=torch.float32, device=x2.device)
         rstd = torch.empty(rows, dtype=torch.float32, device=x2.device)
-    with torch.cuda.device(x2.device):
+    with _ffi.device_guard(x2.device):
         _ffi.check(_ffi.lib().scree_layernorm_fwd(
             _ffi.ptr(x2), _ffi.ptr(w), _ffi.ptr(b), _ffi.ptr(y), _ffi.ptr(mean), _ffi.ptr(rstd),
             rows, d, float(eps), _ffi.dtype_code(x2.dtype), _ffi.stream_of(x2)))
@@ -83,7 +83,7 @@ def rmsnorm_bwd(dy2, x2, w, rstd, want_dw, dw_like=None):
         code = _dparam_code(dw_like) if dw_like is not None else _ffi.DTYPE_F32
         dw = torch.empty(d, dtype=_code_dtype(code), device=x2.device)
     ws = _workspace(rows, d, x2.device)
-    with torch.cuda.device(x2.device):
+    with _ffi.device_guard(x2.device):
         _ffi.check(_ffi.lib().scree_rmsnorm_bwd(
             _ffi.ptr(dy2), _ffi.ptr(x2), _ffi.ptr(w), _ffi.ptr(rstd), _ffi.ptr(dx), _ffi.ptr(dw),
             code, rows, d, _ffi.dtype_code(x2.dtype), _ffi.ptr(ws), ws.numel(),
@@ -98,7 +98,7 @@ def layernorm_bwd(dy2, x2, w, mean, rstd, want_dw, want_db, p_like=None):
     dw = torch.empty(d, dtype=_code_dtype(code), device=x2.device) if want_dw else None
     db = torch.empty(d, dtype=_code_dtype(code), device=x2.device) if want_db else None
     ws = _workspace(rows, d, x2.device)
-    with torch.cuda.device(x2.device):
+    with _ffi.device_guard(x2.device):
         _ffi.check(_ffi.lib().scree_layernorm_bwd(
             _ffi.ptr(dy2), _ffi.ptr(x2), _ffi.ptr(w), _ffi.ptr(mean), _ffi.ptr(rstd),
             _ffi.ptr(dx), _ffi.ptr(dw), _ffi.ptr(db), code, rows, d, _ffi.dtype_code(x2.dtype),
@@ -111,7 +111,7 @@ def add_rmsnorm_fwd(x2, r2, w, eps, want_stats):
     h = torch.empty_like(x2)
     y = torch.empty_like(x2)
     rstd = torch.empty(rows, dtype=torch.float32, device=x2.device) if want_stats else None
-    with torch.cuda.device(x2.device):
+    with _ffi.device_guard(x2.device):
         _ffi.check(_ffi.lib().scree_add_rmsnorm_fwd(
             _ffi.ptr(x2), _ffi.ptr(r2), _ffi.ptr(w), _ffi.ptr(h), _ffi.ptr(y), _ffi.ptr(rstd),
             rows, d, float(eps), _ffi.dtype_code(x2.dtype), _ffi.stream_of(x2)))
@@ -127,7 +127,7 @@ def add_rmsnorm_bwd(dy2, dh2, h2, w, rstd, want_dw, dw_like=None):
         code = _dparam_code(dw_like) if dw_like is not None else _ffi.DTYPE_F32
         dw = torch.empty(d, dtype=_code_dtype(code), device=h2.device)
     ws = _workspace(rows, d, h2.device)
-    with torch.cuda.device(h2.device):
+    with _ffi.device_guard(h2.device):
         _ffi.check(_ffi.lib().scree_add_rmsnorm_bwd(
             _ffi.ptr(dy2), _ffi.ptr(dh2), _ffi.ptr(h2), _ffi.ptr(w), _ffi.ptr(rstd), _ffi.ptr(dx),
             _ffi.ptr(dw), code, rows, d, _ffi.dtype_code(h2.dtype), _ffi.ptr(ws), ws.numel(),

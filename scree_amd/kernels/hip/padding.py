@@ -54,7 +54,7 @@ def to_padded_hip(values, offsets, side="right", fill_value=0.0, max_len=None):
     padded = torch.empty((batch, max_len, *feat), dtype=vals.dtype, device=vals.device)
     mask = torch.empty((batch, max_len), dtype=torch.bool, device=vals.device)
     fill, elem = _fill_bytes(fill_value, vals.dtype)
-    with torch.cuda.device(vals.device):
+    with _ffi.device_guard(vals.device):
         _ffi.check(_ffi.lib().scree_to_padded(
             _ffi.ptr(vals), _ffi.ptr(off), batch, vals.shape[0], max_len, _row_bytes(vals, 1),
             1 if side == "left" else 0, ctypes.cast(fill, ctypes.c_void_p), elem,
@@ -72,7 +72,7 @@ def from_padded_hip(padded, mask):
     m = mask.to(device=padded.device, dtype=torch.bool).contiguous()
     pad = padded.contiguous()
     offsets = torch.empty(batch + 1, dtype=torch.int32, device=pad.device)
-    with torch.cuda.device(pad.device):
+    with _ffi.device_guard(pad.device):
         _ffi.check(_ffi.lib().scree_padded_offsets(
             _ffi.ptr(m), batch, t, _ffi.ptr(offsets), _ffi.stream_of(pad)))
         total = int(offsets[-1].item())

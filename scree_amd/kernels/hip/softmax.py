@@ -41,7 +41,7 @@ def softmax_fwd(x, cu_seqlens, out=None):
     f = _features(xc)
     if xc.numel() == 0:
         return y
-    with torch.cuda.device(xc.device):
+    with _ffi.device_guard(xc.device):
         _ffi.check(_ffi.lib().scree_varlen_softmax(
             _ffi.ptr(xc), _ffi.ptr(y), _ffi.ptr(cu_seqlens), cu_seqlens.numel() - 1,
             xc.shape[0], f, _ffi.dtype_code(xc.dtype), _ffi.stream_of(xc)))
@@ -53,7 +53,7 @@ def softmax_bwd(y, dy, cu_seqlens):
     dx = torch.empty_like(yc)
     if yc.numel() == 0:
         return dx
-    with torch.cuda.device(yc.device):
+    with _ffi.device_guard(yc.device):
         _ffi.check(_ffi.lib().scree_varlen_softmax_bwd(
             _ffi.ptr(yc), _ffi.ptr(dyc), _ffi.ptr(dx), _ffi.ptr(cu_seqlens), cu_seqlens.numel() - 1,
             yc.shape[0], _features(yc), _ffi.dtype_code(yc.dtype), _ffi.stream_of(yc)))
