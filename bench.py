@@ -182,9 +182,13 @@ class AttnCase:
         self.ws = torch.empty(A.bwd_workspace_bytes(len(cfg.lengths), n, h, hk, d), dtype=torch.uint8,
                               device=dev)
 
+    def needs_schedule(self) -> bool:
+        return self.A.needs_schedule(len(self.cfg.lengths), self.cfg.total, self.cfg.heads,
+                                     self.cfg.head_dim)
+
     def schedule(self):
-        """The work list, as the user-facing calls build it (nothing for a
-        launch small enough that its workgroups derive their own items)."""
+        """The work list, as the user-facing calls build it (nothing when the
+        forward derives its items and publishes the list itself)."""
         self.A.prepare_workspace(self.cu, self.cfg.total, self.cfg.head_dim, self.cfg.causal,
                                  self.cfg.heads, self.ws)
 
@@ -233,7 +237,8 @@ def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False, kv_hea
            "eager_tflops": flops / (eager_ms * 1e-3) / 1e12, "graph1_ms": graph1_ms}
     res["mfma_frac"] = res["tflops"] / PEAK_F16_TFLOPS
     if per_kernel:
-        kernels = {"attn_schedule": case.schedule, "attn_fwd": case.fwd}
+        kernels = {"attn_schedule": case.schedule} if case.needs_schedule() else {}
+        kernels["attn_fwd"] = case.fwd
         if backward:
             kernels.update({"attn_bwd_dq": case.bwd_dq, "attn_bwd_dkv": case.bwd_dkv})
         res["kernels_ms"] = {k: _graph_time(f, 10, max(3, steps // 5)) for k, f in kernels.items()}

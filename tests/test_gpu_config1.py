@@ -112,6 +112,19 @@ def test_failed_schedule_writes_nan_outputs():
     for name, t in (("out", out), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv),
                     ("delta", delta)):
         assert torch.isnan(t).all(), f"{name} was not filled with NaN"
+    # the forward derives its items here and publishes the failure in the
+    # header of its workspace, which the backward passes then read
+    from scree_amd.kernels.hip import attention as A
+
+    say("case: failed schedule published by the forward -> NaN gradients")
+    ws = torch.full((A.workspace_bytes(3, n, 64),), 255, dtype=torch.uint8, device="cuda")
+    out2, lse2 = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True, workspace=ws)
+    dq2, dk2, dv2 = varlen_attention_hip_backward(do, q, k, v, q, lse2.nan_to_num(0.0), cu,
+                                                  causal=True, workspace=ws)
+    torch.cuda.synchronize()
+    assert ws[:16].view(torch.int32).tolist() == [0, -1, 128, 1]
+    for name, t in (("out", out2), ("lse", lse2), ("dq", dq2), ("dk", dk2), ("dv", dv2)):
+        assert torch.isnan(t).all(), f"{name} was not filled with NaN"
 
 
 def test_backward_rejects_a_wrong_delta_buffer():
