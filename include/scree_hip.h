@@ -107,8 +107,10 @@ size_t scree_attn_bwd_workspace_bytes_gqa(int batch, int64_t total_tokens, int h
  * flag when scree_attn_needs_schedule returns 1, and the backward calls
  * unless a forward on the same workspace came first (calling it anyway is
  * harmless); the workspace may then be reused by any number of forward and
- * backward calls.  No counterpart in the reference (its grid is padded,
- * src/scree/kernels/triton/varlen_attention.py:236). */
+ * backward calls.  A call that reads a workspace neither wrote gives wrong
+ * results but never reads or writes outside its tensors: the kernels skip
+ * items that no schedule can hold.  No counterpart in the reference (its
+ * grid is padded, src/scree/kernels/triton/varlen_attention.py:236). */
 int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_tokens,
                         int head_dim, int causal, void* workspace, size_t workspace_bytes,
                         void* stream);

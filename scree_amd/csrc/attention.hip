@@ -439,15 +439,22 @@ __device__ __forceinline__ ItemView item_view(const ItemSource& src, int tmax) {
   if (MAY_DERIVE && src.derive) v.w = wave_sched(src.cu, src.batch, src.total_tokens);
   const bool derive = MAY_DERIVE && src.derive;
   v.failed = derive ? v.w.total > tmax : listed_batch < 0;
-  v.count = derive ? (v.failed ? 0 : v.w.total) : listed_count;
+  v.count = derive ? (v.failed ? 0 : v.w.total) : min(max(listed_count, 0), tmax);
   return v;
 }
+// On the list path an item that no schedule can have written -- a workspace
+// handed to a backward call before any schedule or forward call filled it --
+// comes out empty (len 0), and the kernels skip it: wrong results for a
+// misused workspace, never an access outside the tensors.
 template <bool MAY_DERIVE>
 __device__ __forceinline__ int4 item_at(const ItemSource& src, const ItemView& v, bool causal, int p) {
   const int4 listed = src.items[p];
   int4 it = make_int4(0, 0, 0, 0);
   if (MAY_DERIVE && src.derive) it = wave_item(v.w, src.batch, causal, src.seq_major != 0, p);
-  return MAY_DERIVE && src.derive ? it : listed;
+  const int4 sel = MAY_DERIVE && src.derive ? it : listed;  // a derived item always passes
+  const bool ok = sel.z >= 0 && sel.w >= 1 && sel.z <= src.total_tokens - sel.w && sel.y >= 0 &&
+                  (int64_t)sel.y * kBM < sel.w;
+  return ok ? sel : make_int4(0, 0, 0, 0);
 }
 
 // The deriving forward's share of the schedule: the last block (the
@@ -1048,6 +1055,7 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
   }
   const int hk = h / group;  // K/V head of this query head
   const int4 it = item_at<true>(src, iv, CAUSAL, item);
+  if (it.w == 0) return;
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   FwdState<T, D> st;
   st.wave = wave_id();
@@ -1309,6 +1317,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) return;
   const int hk = h / group;  // K/V head of this query head
   const int4 it = item_at<false>(src, iv, CAUSAL, item);
+  if (it.w == 0) return;
   const int start = it.z, L = it.w, q0 = it.y * kBM;
   DqState<T, D> st;
   st.wave = wave_id();
@@ -1577,6 +1586,7 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(
   const ItemView iv = item_view<false>(src, tmax);  // a failed schedule: the pass poisoned dk / dv
   if (item >= iv.count) return;
   const int4 it = item_at<false>(src, iv, causal != 0, item);
+  if (it.w == 0) return;
   const int start = it.z, L = it.w;
   const int k0 = ((L + kBM - 1) / kBM - 1 - it.y) * kBM;
   constexpr int C4 = D / 4;
@@ -1648,6 +1658,7 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   const int g0 = part * group / gsplit, g1 = (part + 1) * group / gsplit;
   const int heads = kv_heads * group;
   const int4 it = item_at<false>(src, iv, CAUSAL, item);
+  if (it.w == 0) return;
   const int start = it.z, L = it.w;
   const int nblk = (L + kBM - 1) / kBM;
   const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
@@ -1858,9 +1869,9 @@ inline ItemSource fwd_item_source(void* ws, const int32_t* cu, int batch, int to
                     derive ? static_cast<int32_t*>(ws) : nullptr, batch, total, head_major,
                     derive ? 1 : 0};
 }
-inline ItemSource list_item_source(const void* ws, int tmax, int head_major) {
+inline ItemSource list_item_source(const void* ws, int total, int tmax, int head_major) {
   return ItemSource{static_cast<const int32_t*>(ws), schedule_list(ws, tmax, head_major), nullptr,
-                    nullptr, 0, 0, head_major, 0};
+                    nullptr, 0, total, head_major, 0};
 }
 
 template <typename T, int D, bool C>
@@ -1889,7 +1900,7 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
                      static_cast<const T*>(dout), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<const T*>(o), lse, delta, static_cast<T*>(dq),
-                     list_item_source(ws, tmax, hm), tmax, hm, heads,
+                     list_item_source(ws, total, tmax, hm), tmax, hm, heads,
                      heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
@@ -1905,7 +1916,7 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
   // one workgroup per (item, K/V head, part of the head group)
   const int64_t grid = (int64_t)tmax * kv_heads * gsplit;
   const int hm = attn_head_major(kv_heads * gsplit, tmax);
-  const ItemSource src = list_item_source(ws, tmax, hm);
+  const ItemSource src = list_item_source(ws, total, tmax, hm);
   // the split epilogue has a kernel of its own: its registers would cost the
   // unsplit kernel a wave per SIMD at D = 64
   // (a split group never has the many rounds of a head-major launch)

@@ -256,6 +256,36 @@ def test_backward_reads_the_forwards_lists():
             assert torch.equal(a, b)
 
 
+def test_backward_skips_items_no_schedule_wrote():
+    """A backward handed a workspace whose list no schedule or forward wrote
+    (crafted here: every item out of range in one of the ways the kernels
+    check, the count past the grid) skips those items -- no access outside
+    the tensors, the outputs left exactly as they were."""
+    from scree_amd.kernels.hip import attention as A
+
+    lengths = [300, 17, 129]
+    n = sum(lengths)
+    say(f"case: unscheduled workspace B={len(lengths)} N={n}")
+    off, cu = cu_of(lengths)
+    q, k, v, do = (randn((n, 2, 64), torch.float16, 80 + i) for i in range(4))
+    o, lse = (torch.zeros((n, 2, 64), dtype=torch.float16, device="cuda"),
+              torch.zeros((n, 2), dtype=torch.float32, device="cuda"))
+    ws = A.attention_schedule(cu, n, 64, True)
+    tmax = (n + 127) // 128 + len(lengths)
+    bad = [(0, 0, -5, 10), (0, 0, 0, 0), (0, 0, n - 6, 10), (0, 3, 0, 300), (0, -1, 0, 300),
+           (0, 0, 2 ** 30, 2 ** 30), (0, 0, 0, 2 ** 31 - 1)]
+    items = torch.tensor([bad[p % len(bad)] for p in range(2 * tmax)], dtype=torch.int32)
+    header = torch.tensor([tmax + 100, len(lengths), 128, 1], dtype=torch.int32)
+    ws[:16].copy_(header.view(torch.uint8).cuda())
+    ws[16:16 + 32 * tmax].copy_(items.view(torch.uint8).reshape(-1).cuda())
+    outs = [torch.full_like(q, 7.0) for _ in range(3)]
+    delta = torch.full((n, 2), 7.0, dtype=torch.float32, device="cuda")
+    A._attn_bwd(do, q, k, v, o, lse, cu, True, *outs, delta, ws)
+    torch.cuda.synchronize()
+    for t in outs + [delta]:
+        assert bool((t == 7.0).all())
+
+
 def test_config3_fixed_list_fp16_causal():
     c = workloads.config3(fixed=True)
     _run_case(c.lengths, c.heads, c.head_dim, torch.float16, True, seed=3)
