@@ -164,3 +164,29 @@ def test_cpu_tensors_are_rejected_by_the_hip_path():
         varlen_rmsnorm(arr)
     with pytest.raises(TypeError, match="ROCm"):
         varlen_attention(arr, arr, arr)
+
+
+def test_host_call_helpers():
+    """The argument helpers hand the C ABI plain integers and cached array types."""
+    import torch
+
+    assert _ffi.ptr(None) == 0
+    t = torch.zeros(4)
+    assert _ffi.ptr(t) == t.data_ptr()
+    a = _ffi.int64_array((3, -1, 2 ** 40))
+    b = _ffi.int64_array((7, 8, 9))
+    assert type(a) is type(b) and list(a) == [3, -1, 2 ** 40]
+    assert list(_ffi.int64_array(t.stride()[:1] + (5,))) == [1, 5]
+    # no device switch is entered for a tensor without a device index
+    with _ffi.device_guard(torch.device("cpu")):
+        pass
+
+
+def test_size_queries_are_cached():
+    from scree_amd.kernels.hip import attention as A
+
+    A.workspace_bytes.cache_clear()
+    assert A.workspace_bytes(16, 12160, 64) == A.workspace_bytes(16, 12160, 64)
+    assert A.workspace_bytes.cache_info().hits >= 1
+    assert A.needs_schedule(16, 12160, 16, 64) is False
+    assert A.needs_schedule(65, 1024, 1, 64) is True
