@@ -414,7 +414,7 @@ struct ItemSource {
   const int32_t* header;
   const int4* items;  // the list this launch reads
   const int32_t* cu;
-  int32_t* publish;   // workspace the deriving forward writes the lists into
+  int32_t* publish;   // workspace the deriving forward writes header and list into
   int batch, total_tokens;
   int seq_major;      // the sequence-major list (head-major launches)
   int derive;         // derive items from cu (the forward, batch <= kWaveSched)
@@ -1024,7 +1024,7 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
 
 // Waves per SIMD the forward is compiled for: four (128 registers) for the
 // causal form up to head_dim 64, which fits them without spills; two
-// otherwise (the compiler then takes what it needs: 134 registers, three
+// otherwise (the compiler then takes what it needs: ~135 registers, three
 // waves, for the non-causal form at 64).
 template <int D, bool CAUSAL>
 constexpr int attn_fwd_waves() {
@@ -1849,12 +1849,12 @@ inline const int4* schedule_list(const void* ws, int tmax, int head_major) {
   return reinterpret_cast<const int4*>(static_cast<const char*>(ws) + kHeaderBytes) +
          (head_major ? tmax : 0);
 }
-// The forward derives its items (and publishes the lists) for batches of at
+// The forward derives its items (and publishes its list) for batches of at
 // most kWaveSched sequences in launches of a few rounds of workgroups; the
 // backward passes read the lists.  Deriving costs each round of workgroups
 // ~0.6 us at head_dim <= 64 (four or three workgroups per CU) and ~1.2 us at
 // 128 (two): config 4's 1,776 workgroups pay +1.0 us against the scheduler's
-// 3.4, config 5's 23,040 at head_dim 128 +55 us.
+// 3.4, config 5's 22,048 at head_dim 128 +55 us.
 constexpr int64_t kFwdDeriveMaxBlocks = 2048;  // 1024 at head_dim 128
 static_assert(kFwdDeriveMaxBlocks < (int64_t)kXcds * 512,
               "a deriving forward's problem must have no head-major pass (attn_head_major)");

@@ -11,11 +11,12 @@
 // or rows longer than the fast path holds): one wavefront per row looping
 // over the columns.
 //
-// Backward writes dx per row and accumulates the parameter gradients in fp32
-// registers of each wave over the rows it owns; the waves of a block then sum
-// their partials in LDS in a fixed order and write one partial row per block;
-// a column-sum kernel adds the partial rows in a fixed order.  No atomics:
-// results are bit-identical from run to run.
+// Backward (norm_bwd_cols): each thread of a block owns fixed 16-byte column
+// vectors across the block's rows, so the parameter gradients accumulate in
+// its fp32 registers; the row statistics are reduced across the block through
+// LDS, dx is written per row, and each block writes one partial row of
+// parameter gradients, which a column-sum kernel adds in a fixed order.  No
+// atomics: results are bit-identical from run to run.
 #include <initializer_list>
 
 #include "common.h"
