@@ -231,7 +231,8 @@ def test_forward_publishes_the_schedule(causal):
         np.testing.assert_array_equal(ig.numpy(), iw.numpy())
 
 
-def test_backward_reads_the_forwards_lists():
+@pytest.mark.parametrize("causal", [True, False])
+def test_backward_reads_the_forwards_lists(causal):
     """Forward then backward on one workspace of stale bytes, no schedule
     call: the same outputs and gradients, bit for bit, as the standalone
     backward, which schedules its own workspace."""
@@ -240,15 +241,15 @@ def test_backward_reads_the_forwards_lists():
 
     for lengths, heads in (([300, 17, 129, 640, 1, 0, 77], 4), (workloads.config4().lengths, 16)):
         n = sum(lengths)
-        say(f"case: forward-built lists B={len(lengths)} N={n} H={heads}")
+        say(f"case: forward-built lists B={len(lengths)} N={n} H={heads} causal={causal}")
         off, cu = cu_of(lengths)
         q, k, v, do = (randn((n, heads, 64), torch.float16, 50 + i) for i in range(4))
-        ref = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
-        ref_g = varlen_attention_hip_backward(do, q, k, v, ref[0], ref[1], cu, causal=True)
+        ref = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True)
+        ref_g = varlen_attention_hip_backward(do, q, k, v, ref[0], ref[1], cu, causal=causal)
         stale = torch.full((A.workspace_bytes(len(lengths), n, 64),), 255, dtype=torch.uint8,
                            device="cuda")
-        got = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True, workspace=stale)
-        got_g = varlen_attention_hip_backward(do, q, k, v, got[0], got[1], cu, causal=True,
+        got = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True, workspace=stale)
+        got_g = varlen_attention_hip_backward(do, q, k, v, got[0], got[1], cu, causal=causal,
                                               workspace=stale)
         torch.cuda.synchronize()
         assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
