@@ -6,7 +6,8 @@
 Primary line: causal varlen attention forward +
 backward, fp16, 16 sequences summing to 12160 tokens (log-normal, sigma 0.6,
 rescaled), 16 heads x head_dim 64, synthetic N(0,1) inputs already resident
-in HBM.  One step = tile scheduler + forward (O, LSE) + dQ/Delta pass + dK/dV
+in HBM.  One step = work list (the forward derives and publishes it at this
+size; larger problems launch the tile scheduler) + forward (O, LSE) + dQ/Delta pass + dK/dV
 pass into preallocated buffers.  K steps are replayed from HIP graphs of up
 to 10 consecutive steps (graphs of one step and eager call-by-call launches
 are reported beside it).  Every timed region is preceded by untimed
@@ -215,7 +216,8 @@ class AttnCase:
 
 
 def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False, kv_heads=None):
-    """One step = scheduler + forward (+ dQ + dK/dV) on preallocated buffers.
+    """One step = work list (scheduler launch, or none when the forward derives
+    it) + forward (+ dQ + dK/dV) on preallocated buffers.
 
     ``ms`` times ``steps`` steps replayed from HIP graphs of up to 10
     consecutive steps (HIP events around the replays); ``graph1_ms`` replays
@@ -378,7 +380,7 @@ def time_shape_sweep(steps, warmup):
     """The reference's 27-shape sweep (``benchmarks/modal_multishape_sweep.py:64-69``):
     head_dim 32/64/128 x heads 4/8/16 x mean length 256/1024/2048, 16
     sequences, log-normal sigma 0.6 (seed 0, ``max(1, int(x))``, no clip),
-    causal fp16.  Each row: forward and forward+backward steps (scheduler
+    causal fp16.  Each row: forward and forward+backward steps (work list
     included) on preallocated buffers, replayed from HIP graphs of up to 10
     steps, real-token causal TFLOP/s and fraction of the dense fp16 peak."""
     import torch
@@ -674,7 +676,7 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic N(0,1), resident in HBM",
         "config": {
-            "workload": ("cfg4: causal varlen attention forward+backward (scheduler + fwd + dQ + dK/dV), "
+            "workload": ("cfg4: causal varlen attention forward+backward (fwd with its work list + dQ + dK/dV), "
                          f"fp16, {len(cfg4.lengths)} seqs, {cfg4.total} tokens (log-normal sigma 0.6 "
                          f"rescaled), {cfg4.heads} heads x head_dim {cfg4.head_dim}"),
             "lengths": cfg4.lengths,
