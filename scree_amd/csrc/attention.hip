@@ -741,8 +741,8 @@ __device__ __forceinline__ void poison_stats(float* __restrict__ p, int total, i
 // sum <= kSumLimit bounds every weight by 2^8, which fp32 sums and fp16/bf16
 // operands hold with the same relative precision as values <= 1.  Only when
 // some lane's sum exceeds it (or is NaN) does the wave take the tile maximum,
-// raise m, rescale O and the row sum, and form the weights again -- on the
-// first tile of every item (m starts at -1e30) and rarely after.
+// raise m, rescale O and the row sum, and form the weights again -- rarely:
+// a wave's first tile sets m from the tile itself (fwd_first_weights).
 constexpr float kSumLimit = 256.0f;
 
 // ------------------------------------------------------- tile staging
@@ -880,6 +880,10 @@ struct FwdState {
 // v_max3_f32 written out: for fmaxf the compiler first canonicalises every
 // operand it cannot prove is not a signalling NaN (each MFMA result), one
 // extra instruction each.  Scores are MFMA results or -inf, never signalling.
+// The compiler cannot see inside the asm: it inserts no wait states before
+// it, so its operands must never come straight from an MFMA (whose results a
+// VALU instruction may read only after wait states the compiler adds before
+// instructions it can see).
 __device__ __forceinline__ float max3f(float a, float b, float c) {
   float r;
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
@@ -909,6 +913,21 @@ __device__ __forceinline__ float tile_max(const f32x16& s) {
   float lo, hi;
   half_pair(max3f(ma, mc, mc), lo, hi);
   return max3f(lo, hi, hi);
+}
+
+// tile_max for scores fresh from the MFMAs: the same maximum (max is exact in
+// any order) from maxima the compiler emits itself, so it places the MFMA
+// result wait before the first of them.
+__device__ __forceinline__ float tile_max_fresh(const f32x16& s) {
+  float ma = fmaxf(s[0], s[1]), mb = fmaxf(s[2], s[3]);
+#pragma unroll
+  for (int i = 4; i < 16; i += 2) {
+    ma = fmaxf(ma, s[i]);
+    mb = fmaxf(mb, s[i + 1]);
+  }
+  float lo, hi;
+  half_pair(fmaxf(ma, mb), lo, hi);
+  return fmaxf(lo, hi);
 }
 
 // Mask (to -inf) the keys of the 32-key score tile at tbase that this lane's
@@ -947,6 +966,17 @@ __device__ __forceinline__ void fwd_rescale(FwdState<T, D>& st, const f32x16& s,
   ls = fwd_weights(st, s, p);
 }
 
+// A wave's first tile: O and the row sum are still zero, so the reference
+// maximum comes from the tile directly -- the value fwd_rescale reaches after
+// the sum check against the initial -1e30 fails, without forming the
+// weights twice or rescaling a zero O -- and the weights are formed once.
+template <typename T, int D>
+__device__ __forceinline__ float fwd_first_weights(FwdState<T, D>& st, const f32x16& s, f32x16& p) {
+  st.m_run = fmaxf(st.m_run, tile_max_fresh(s));
+  st.neg_mb = -st.m_run * st.scale_log2;
+  return fwd_weights(st, s, p);
+}
+
 // O^T += V^T P^T for one tile: the weights rounded to T as the B operand,
 // V^T read transposed from the tile's 32 rows at sVt.
 template <typename T, int D>
@@ -968,7 +998,7 @@ __device__ __forceinline__ void fwd_pv(FwdState<T, D>& st, const f32x16& p, cons
 // softmax, whose VALU work then overlaps the second tile's MFMAs.  The
 // restrict qualifiers tell the compiler the two buffers are disjoint, so it
 // keeps the DMA in flight across the reads.
-template <typename T, int D, bool CAUSAL, bool FULL>
+template <typename T, int D, bool CAUSAL, bool FULL, bool FIRST = false>
 __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* __restrict__ cur,
                                           T* __restrict__ nxt) {
   constexpr int TILE = kBN * D;
@@ -990,8 +1020,13 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
       s1 = zero16();
 #pragma unroll
       for (int s = 0; s < D / 16; ++s) s1 = mfma32(lds_frag16(sK + 32 * D + st.koff[s]), st.qf[s], s1);
-      float ls0 = fwd_weights(st, s0, p0);
-      if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+      float ls0;
+      if (FIRST) {
+        ls0 = fwd_first_weights(st, s0, p0);
+      } else {
+        ls0 = fwd_weights(st, s0, p0);
+        if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+      }
       st.l_run += ls0;
       fwd_pv(st, p0, sV);
       float ls1 = fwd_weights(st, s1, p1);
@@ -1005,8 +1040,13 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
         for (int s = 0; s < D / 16; ++s) s1 = mfma32(lds_frag16(sK + 32 * D + st.koff[s]), st.qf[s], s1);
       }
       fwd_mask<T, D, CAUSAL>(st, s0, kbase);
-      float ls0 = fwd_weights(st, s0, p0);
-      if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+      float ls0;
+      if (FIRST) {
+        ls0 = fwd_first_weights(st, s0, p0);
+      } else {
+        ls0 = fwd_weights(st, s0, p0);
+        if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+      }
       st.l_run += ls0;
       fwd_pv(st, p0, sV);
       if (nt > 1) {
@@ -1108,7 +1148,17 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
   // before the item's first query (causal) or before a partial last block.
   // Unrolled by two so that each call sees its buffers at fixed positions.
   const int nfull = CAUSAL ? min(q0, L) / kBN : L / kBN;
-  int kb = 0;
+  // Block 0 (there is always one) holds every live wave's first tile.
+  if (nfull >= 1)
+    fwd_block<T, D, CAUSAL, true, true>(st, 0, bufA, bufB);
+  else
+    fwd_block<T, D, CAUSAL, false, true>(st, 0, bufA, bufB);
+  {
+    T* t = bufA;
+    bufA = bufB;
+    bufB = t;
+  }
+  int kb = 1;
   for (; kb + 1 < nfull; kb += 2) {
     fwd_block<T, D, CAUSAL, true>(st, kb, bufA, bufB);
     fwd_block<T, D, CAUSAL, true>(st, kb + 1, bufB, bufA);
