@@ -523,7 +523,12 @@ __global__ __launch_bounds__(256) void norm_param_colsum4(const float* __restric
                                                           void* out0, void* out1, int out_dtype) {
   __shared__ float4 red[64][4];
   const int cq = threadIdx.x & 3, rg = threadIdx.x >> 2;
-  const int col = blockIdx.x * 16 + cq * 4;
+  // A block reads a 64-byte strip of each partial row; block b runs on XCD
+  // b mod 8, so neighbouring strips (one 128-byte line) go to blocks of the
+  // same XCD, whose L2 then fetches the line once instead of once per XCD.
+  int slab = blockIdx.x;
+  if ((gridDim.x & 7) == 0) slab = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int col = slab * 16 + cq * 4;
   const int p = blockIdx.y;
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
   if (col < dim) {
