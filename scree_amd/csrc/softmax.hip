@@ -114,13 +114,27 @@ __device__ __forceinline__ void sm_merge(float& m, float& l, float m2, float l2)
   m = hi;
 }
 
+// Workgroup -> (sequence, column chunk) index.  Block b runs on XCD b mod 8.
+// When a chunk is narrower than a 128-byte line, the line's two halves
+// (chunks 2k and 2k + 1) go to blocks b and b + 8 of each group of 16, which
+// share an XCD, so its L2 fetches the line once instead of two L2s fetching
+// it; blocks past the last full group of 16 keep their index.  Consecutive
+// pairs still cycle over the XCDs, so every XCD gets a fair share of every
+// sequence.
+__device__ __forceinline__ int sm_block(bool half_lines) {
+  const int b = blockIdx.x;
+  if (!half_lines || b >= (int)(gridDim.x & ~15u)) return b;
+  return (b & ~15) | ((b & 7) << 1) | ((b >> 3) & 1);
+}
+
 template <typename T, int VEC>
 __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
     const T* __restrict__ x, T* __restrict__ y, const int32_t* __restrict__ cu, int64_t total,
     int64_t features, int ct, int chunks) {
   __shared__ float s_m[kSmThreads * VEC];
   __shared__ float s_l[kSmThreads * VEC];
-  const int seq = blockIdx.x / chunks, chunk = blockIdx.x - seq * chunks;
+  const int bsel = sm_block(ct * VEC * (int)sizeof(T) < 128);
+  const int seq = bsel / chunks, chunk = bsel - seq * chunks;
   // offsets are clamped to [0, total]: malformed input cannot index outside x
   const int64_t start = min<int64_t>(max<int64_t>(cu[seq], 0), total);
   const int64_t end = min<int64_t>(max<int64_t>(cu[seq + 1], start), total);
@@ -259,7 +273,8 @@ __global__ __launch_bounds__(kSmThreadsBwd) void varlen_softmax_bwd_kernel(
     const T* __restrict__ y, const T* __restrict__ dy, T* __restrict__ dx,
     const int32_t* __restrict__ cu, int64_t total, int64_t features, int ct, int chunks) {
   __shared__ float s_s[kSmThreadsBwd * VEC];
-  const int seq = blockIdx.x / chunks, chunk = blockIdx.x - seq * chunks;
+  const int bsel = sm_block(ct * VEC * (int)sizeof(T) < 128);
+  const int seq = bsel / chunks, chunk = bsel - seq * chunks;
   const int64_t start = min<int64_t>(max<int64_t>(cu[seq], 0), total);
   const int64_t end = min<int64_t>(max<int64_t>(cu[seq + 1], start), total);
   const int rs = kSmThreadsBwd / ct;
@@ -377,7 +392,7 @@ struct SmShape {
 };
 template <typename T>
 SmShape sm_shape(int64_t features, bool aligned, int batch, int64_t total, int threads,
-                 int cache_rows) {
+                 int cache_rows, int min_ct) {
   constexpr int V = 16 / sizeof(T);
   SmShape sh;
   sh.vec = features % V == 0 && aligned;
@@ -386,10 +401,12 @@ SmShape sm_shape(int64_t features, bool aligned, int batch, int64_t total, int t
   while (sh.ct < units && sh.ct < 64) sh.ct <<= 1;
   // Fewer column lanes -> more chunks, more workgroups, and more row lanes,
   // i.e. longer sequences held in registers: narrow until the grid is large
-  // and cache_rows rows per row lane cover twice the mean sequence length (each
-  // row segment a lane group reads stays >= 8 x 16 bytes contiguous).
+  // and cache_rows rows per row lane cover twice the mean sequence length, to
+  // min_ct lanes at least.  The forward goes down to 4 (64-byte row
+  // segments, half-line chunks paired on one XCD by sm_block); the backward
+  // keeps >= 8 x 16 bytes contiguous.
   const int64_t cover = 2 * ((total + batch - 1) / batch);
-  while (sh.ct > 8 && ((int64_t)batch * ((units + sh.ct - 1) / sh.ct) < kSmMinBlocks ||
+  while (sh.ct > min_ct && ((int64_t)batch * ((units + sh.ct - 1) / sh.ct) < kSmMinBlocks ||
                        (int64_t)cache_rows * (threads / sh.ct) < cover))
     sh.ct >>= 1;
   sh.chunks = (units + sh.ct - 1) / sh.ct;
@@ -402,7 +419,7 @@ int launch_softmax_bwd(const void* y, const void* dy, void* dx, const int32_t* c
   constexpr int V = 16 / sizeof(T);
   const SmShape sh =
       sm_shape<T>(features, aligned16(y) && aligned16(dy) && aligned16(dx), batch, total,
-                  kSmThreadsBwd, kSmCacheBwd);
+                  kSmThreadsBwd, kSmCacheBwd, 8);
   if ((int64_t)batch * sh.chunks > 0x7fffffff)
     return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax_bwd: grid too large");
   const dim3 grid((unsigned)(batch * sh.chunks));
@@ -422,7 +439,7 @@ int launch_softmax(const void* x, void* y, const int32_t* cu, int batch, int64_t
                    int64_t features, hipStream_t stream) {
   constexpr int V = 16 / sizeof(T);
   const SmShape sh = sm_shape<T>(features, aligned16(x) && aligned16(y), batch, total,
-                                 kSmThreads, kSmCache);
+                                 kSmThreads, kSmCache, 4);
   if ((int64_t)batch * sh.chunks > 0x7fffffff)
     return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: grid too large");
   const dim3 grid((unsigned)(batch * sh.chunks));

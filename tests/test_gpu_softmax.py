@@ -50,10 +50,11 @@ def test_softmax_shapes(dtype, features):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_register_capacity_boundary(dtype):
-    """64 features give 8 column lanes: the forward's 32 row lanes hold 16 rows
-    each in registers (512 rows; 513 are re-read), the backward's 64 row lanes
-    10 rows of y and dy (640 rows; 641 are re-read)."""
-    _run([512, 513, 640, 641, 3], (64,), dtype, seed=11)
+    """64 features: the forward narrows to 4 column lanes (half-line chunks,
+    paired on one XCD), whose 64 row lanes hold 16 rows each in registers
+    (1,024 rows; 1,025 are re-read); the backward stops at 8 column lanes,
+    whose 64 row lanes hold 10 rows of y and dy (640 rows; 641 are re-read)."""
+    _run([512, 513, 640, 641, 1024, 1025, 3], (64,), dtype, seed=11)
 
 
 def test_rows_sum_to_one_and_masked_entries():
