@@ -702,9 +702,14 @@ struct Strides {
 // stays in that XCD's L2.
 constexpr int kXcds = 8;
 
+// pair (sequence-major, rows of head_dim narrower than a 128-byte line, no
+// grouped K/V): heads 2m and 2m + 1 of a token share a line, so the logical
+// blocks 2k and 2k + 1 run as blocks b and b + 8 of each group of 16, which
+// share an XCD and its L2 (block b runs on XCD b mod 8); blocks past the last
+// full group of 16 keep their index.
 __device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, int group,
-                                          int& item, int& head) {
-  const int b = blockIdx.x;
+                                          bool pair, int& item, int& head) {
+  int b = blockIdx.x;
   if (head_major) {
     const int x = b % kXcds, j = b / kXcds;
     const int k = j / tmax;  // k-th head of this XCD
@@ -712,6 +717,7 @@ __device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, i
     head = x + kXcds * k;
     if (head >= heads) return false;
   } else {
+    if (pair && b < (int)(gridDim.x & ~15u)) b = (b & ~15) | ((b & 7) << 1) | ((b >> 3) & 1);
     item = b / heads;
     head = b % heads;
   }
@@ -1089,7 +1095,8 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
     return;
   }
   int item, h;
-  if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) {
+  if (!map_block(heads, tmax, head_major, group, D * (int)sizeof(T) < 128 && group == 1, item, h) ||
+      item >= iv.count) {
     publish_header(src, iv, CAUSAL ? 1 : 0);
     return;
   }
@@ -1364,7 +1371,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     return;
   }
   int item, h;
-  if (!map_block(heads, tmax, head_major, group, item, h) || item >= iv.count) return;
+  if (!map_block(heads, tmax, head_major, group, D * (int)sizeof(T) < 128 && group == 1, item, h) ||
+      item >= iv.count)
+    return;
   const int hk = h / group;  // K/V head of this query head
   const int4 it = item_at<false>(src, iv, CAUSAL, item);
   if (it.w == 0) return;
@@ -1703,7 +1712,10 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
     return;
   }
   int item, hv;
-  if (!map_block(kv_heads * gsplit, tmax, head_major, 1, item, hv) || item >= iv.count) return;
+  if (!map_block(kv_heads * gsplit, tmax, head_major, 1, D * (int)sizeof(T) < 128 && group == 1, item,
+                 hv) ||
+      item >= iv.count)
+    return;
   const int hk = hv % kv_heads, part = hv / kv_heads;
   const int g0 = part * group / gsplit, g1 = (part + 1) * group / gsplit;
   const int heads = kv_heads * group;
