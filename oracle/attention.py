@@ -168,3 +168,106 @@ def attention_bwd(do, q, k, v, o, lse, offsets, causal=False, dtype=np.float64, 
             dq[s:e] = scale * np.matmul(ds, ki.transpose(1, 0, 2)).transpose(1, 0, 2)
             dk[s:e] = scale * np.matmul(ds.transpose(0, 2, 1), qi.transpose(1, 0, 2)).transpose(1, 0, 2)
     return dq, _fold_kv(dk, kv_heads), _fold_kv(dv, kv_heads), delta
+
+
+def _rounder(operand):
+    """Rounding of an fp32 value to the kernel operand type, returned as fp64."""
+    if operand in (None, "float64"):
+        return lambda x: x
+    if operand == "float32":
+        return lambda x: np.asarray(x, dtype=np.float32).astype(np.float64)
+    if operand == "float16":
+        return lambda x: np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float64)
+    if operand == "bfloat16":
+        from .norms import round_bf16
+        return round_bf16
+    raise ValueError(f"unknown operand type {operand}")
+
+
+def attention_fwd_rounded(q, k, v, offsets, causal=False, operand="float16", block=64):
+    """``(O, LSE)`` with the reference GPU forward's own roundings.
+
+    Restates the loop of ``src/scree/kernels/triton/varlen_attention.py:105-162``:
+    per 64-key block, the running maximum ``m_new = max(m, rowmax(S_blk))``,
+    ``alpha = exp(m - m_new)``, ``p = exp(S_blk - m_new)``, ``l = alpha*l +
+    rowsum(p)`` (unrounded ``p``), ``acc = alpha*acc + round(p) @ V_blk``
+    (``p.to(v.dtype)``, ``:142``), then ``O = round(acc / l)`` and ``LSE = m +
+    log(l)``.  ``round`` is the cast to ``operand``; everything else is fp64
+    (the reference keeps it in fp32).  With ``operand="float64"`` this is
+    :func:`attention_fwd` up to summation order.
+    """
+    rnd = _rounder(operand)
+    off = np.asarray(offsets, dtype=np.int64)
+    q = np.asarray(q, dtype=np.float64)
+    k = _expand_kv(np.asarray(k, dtype=np.float64), q.shape[1])
+    v = _expand_kv(np.asarray(v, dtype=np.float64), q.shape[1])
+    n, h, d = q.shape
+    scale = 1.0 / math.sqrt(d)
+    out = np.zeros_like(q)
+    lse = np.zeros((n, h))
+    for i in range(len(off) - 1):
+        s, e = int(off[i]), int(off[i + 1])
+        length = e - s
+        if length <= 0:
+            continue
+        scores = _scores(q[s:e], k[s:e], scale, "matmul")  # (H, L, L)
+        if causal:
+            scores = np.where(np.triu(np.ones((length, length), dtype=bool), k=1), -np.inf, scores)
+        vt = v[s:e].transpose(1, 0, 2)
+        m = np.full((h, length, 1), -np.inf)
+        l = np.zeros((h, length, 1))
+        acc = np.zeros((h, length, d))
+        with np.errstate(invalid="ignore"):
+            for j in range(0, length, block):
+                sb = scores[:, :, j:j + block]
+                m_new = np.maximum(m, sb.max(axis=-1, keepdims=True))
+                alpha = np.exp(m - m_new)  # 0 on the first block (m = -inf)
+                p = np.exp(sb - m_new)
+                l = alpha * l + p.sum(axis=-1, keepdims=True)
+                acc = alpha * acc + np.matmul(rnd(p), vt[:, j:j + block])
+                m = m_new
+        out[s:e] = rnd(acc / l).transpose(1, 0, 2)
+        lse[s:e] = (m + np.log(l))[..., 0].T
+    return out, lse
+
+
+def attention_bwd_rounded(do, q, k, v, o, lse, offsets, causal=False, operand="float16"):
+    """``(dQ, dK, dV, Delta)`` with the reference GPU backward's own roundings.
+
+    Restates ``src/scree/kernels/triton/_backward.py``: ``Delta = rowsum(O*dO)``
+    from the stored O (``:53-69``); ``P = exp(S - LSE)``; ``dV += round(P)^T dO``
+    (``p.to(do.dtype)``, ``:174``); ``dS = P*(dP - Delta)``; ``dK += scale *
+    round(dS)^T Q`` (``:181``) and ``dQ += scale * round(dS) K`` (``:282``);
+    the three results rounded to ``operand`` when stored.  Grouped-query
+    gradients are summed over each group before that rounding, as the HIP
+    dK/dV pass does.  Sums run in fp64 (the reference: fp32).
+    """
+    rnd = _rounder(operand)
+    off = np.asarray(offsets, dtype=np.int64)
+    do = np.asarray(do, dtype=np.float64)
+    q = np.asarray(q, dtype=np.float64)
+    kv_heads = np.shape(k)[1]
+    k = _expand_kv(np.asarray(k, dtype=np.float64), q.shape[1])
+    v = _expand_kv(np.asarray(v, dtype=np.float64), q.shape[1])
+    o = np.asarray(o, dtype=np.float64)
+    lse = np.asarray(lse, dtype=np.float64)
+    n, h, d = q.shape
+    scale = 1.0 / math.sqrt(d)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    delta = (o * do).sum(axis=-1)
+    for i in range(len(off) - 1):
+        s, e = int(off[i]), int(off[i + 1])
+        length = e - s
+        if length <= 0:
+            continue
+        qi, ki, vi, doi = (t[s:e].transpose(1, 0, 2) for t in (q, k, v, do))
+        scores = np.matmul(qi, ki.transpose(0, 2, 1)) * scale
+        if causal:
+            scores = np.where(np.triu(np.ones((length, length), dtype=bool), k=1), -np.inf, scores)
+        p = np.exp(scores - lse[s:e].T[:, :, None])
+        dv[s:e] = np.matmul(rnd(p).transpose(0, 2, 1), doi).transpose(1, 0, 2)
+        dp = np.matmul(doi, vi.transpose(0, 2, 1))
+        ds = rnd(p * (dp - delta[s:e].T[:, :, None]))
+        dq[s:e] = scale * np.matmul(ds, ki).transpose(1, 0, 2)
+        dk[s:e] = scale * np.matmul(ds.transpose(0, 2, 1), qi).transpose(1, 0, 2)
+    return rnd(dq), rnd(_fold_kv(dk, kv_heads)), rnd(_fold_kv(dv, kv_heads)), delta

@@ -860,6 +860,35 @@ __device__ __forceinline__ float halves_sum(float x) {
   return a + b;
 }
 
+// bf16 forward: O is normalised by the sum of the weights as rounded into the
+// P operand, while the LSE keeps the sum of the unrounded weights (as the
+// reference's l, triton/varlen_attention.py:138).  The weights here are taken
+// against a reference maximum that may lag the row's true maximum by up to
+// 2^8 (kSumLimit), so a row's dominant weight is an arbitrary value in
+// (1, 256] whose bf16 rounding (2^-9 relative) would otherwise pass straight
+// into O; the reference's dominant weight is exp(0) = 1, exact.  Dividing by
+// the operand sum makes O a convex combination of V rows with the rounded
+// weights, in which a dominant weight's rounding cancels.  (fp16 rounds 8x
+// finer; its budget holds without the second sum.)  Cost: 8 v_dot2 per tile.
+template <typename T>
+constexpr bool fwd_operand_sum() {
+  return std::is_same<T, bf16>::value;
+}
+// acc + the sum of the 16 bf16 weights packed in two MFMA operands.
+template <typename X8>
+__device__ __forceinline__ float operand_sum(const X8& a, const X8& b, float acc) {
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+  const uint4 ua = __builtin_bit_cast(uint4, a), ub = __builtin_bit_cast(uint4, b);
+  const uint32_t w[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+  float x = acc, y = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    x = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), one, x, false);
+    y = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i + 1]), one, y, false);
+  }
+  return x + y;
+}
+
 // Running max starts finite: the first tile always rescales (by exp2 of a
 // huge negative number, i.e. 0), and no -inf special case is needed.
 constexpr float kMaxInit = -1e30f;
@@ -874,6 +903,7 @@ struct FwdState {
   int2 voffs[D / 32];       // swizzled V transposed-read offsets
   f32x16 oacc[D / 32];      // O^T accumulators
   float m_run, l_run;       // reference max (raw scores) and row sum (this lane's keys)
+  float l_op;               // bf16: row sum of the weights as rounded into the P operand
   float neg_mb;             // -m_run * scale_log2
   DmaTile<T, D, kBN> dK, dV;
   const T* kh;
@@ -963,6 +993,7 @@ __device__ __forceinline__ void fwd_rescale(FwdState<T, D>& st, const f32x16& s,
   const float m_new = fmaxf(st.m_run, tile_max(s));
   const float alpha = fast_exp2((st.m_run - m_new) * st.scale_log2);
   st.l_run *= alpha;
+  if constexpr (fwd_operand_sum<T>()) st.l_op *= alpha;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -994,6 +1025,7 @@ __device__ __forceinline__ void fwd_pv(FwdState<T, D>& st, const f32x16& p, cons
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
     st.oacc[dt] = mfma32(lds_frag_tr(sVt + 16 * D, st.voffs[dt]), pf1, st.oacc[dt]);
+  if constexpr (fwd_operand_sum<T>()) st.l_op = operand_sum(pf0, pf1, st.l_op);
 }
 
 // One 64-key block kb: start the DMA of block kb + 1 into `nxt`, then compute
@@ -1147,6 +1179,7 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
   for (int dt = 0; dt < D / 32; ++dt) st.oacc[dt] = zero16();
   st.m_run = kMaxInit;
   st.l_run = 0.f;
+  st.l_op = 0.f;
   st.neg_mb = -kMaxInit * scale_log2;
 
   __builtin_amdgcn_s_waitcnt(0);
@@ -1183,7 +1216,7 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
   }
   if (wave_live) {  // the last block's barrier freed the tile buffers: stage O there
     const float l_tot = halves_sum(st.l_run);
-    const float inv_l = 1.0f / l_tot;
+    const float inv_l = 1.0f / (fwd_operand_sum<T>() ? halves_sum(st.l_op) : l_tot);
     store_rows_staged<T, D>(smem + st.wave * stage_elems<D>(), st.oacc, inv_l,
                             o + (int64_t)(start + st.qw0) * so.row + (int64_t)h * so.head, so.row,
                             min(32, L - st.qw0), st.lr, st.g, lane);
@@ -1193,31 +1226,6 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
   // last: a store issued earlier would hold up the prologue's counter waits
   publish_header(src, iv, CAUSAL ? 1 : 0);
   if (h == 0) publish_item(src, item, it);
-}
-
-// ------------------------------------------- dQ pass: folded score scale
-// The dQ pass needs P = 2^(s * scale*log2(e) - LSE*log2(e)) per score.  In
-// fp16 the factor c = scale*log2(e) is folded into the Q rows it holds in
-// registers (each element multiplied by c in fp32 and rounded once to fp16),
-// and the score accumulator starts at -LSE*log2(e) of the lane's query
-// instead of 0, so the MFMA chain yields the exponent itself and the
-// per-score FMA (16 per 32x32 tile) is gone.  The extra rounding moves an
-// exponent by about 2^-11 * c * sqrt(sum (q_d k_d)^2), a relative error in P
-// below the one fp16 already gives P as an MFMA operand; dQ sums it over one
-// head's keys.  The dK/dV pass keeps the fp32 FMA: its sums run over every
-// query of a head group (8 heads of grouped-query attention), where the
-// same perturbation measured dV 6.9e-3 against the 5e-3 bound.  bf16 (8
-// significant bits) keeps the FMA in both passes.
-template <typename T>
-constexpr bool dq_prescale() {
-  return std::is_same<T, f16>::value;
-}
-template <typename T>
-__device__ __forceinline__ typename VecT<T>::x8 scale_frag(typename VecT<T>::x8 f, float c) {
-  typename VecT<T>::x8 r;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = from_f32<T>((float)f[j] * c);
-  return r;
 }
 
 // -------------------------------------------------- backward: dQ and Delta
@@ -1237,7 +1245,6 @@ struct DqState {
   int2 ktr[D / 32];           // swizzled transposed-read offsets (K^T)
   f32x16 dqacc[D / 32];       // dQ^T accumulators
   f32x16 neg_delta;           // dP^T accumulates onto -Delta: it comes out as dP^T - Delta
-  f32x16 neg_lse;             // fp16: S^T accumulates onto -LSE*log2(e) (Q rows pre-scaled)
   float lse2;                 // this lane's LSE * log2(e)
   DmaTile<T, D, kBN> dK, dV;
   const T* kh;
@@ -1271,11 +1278,10 @@ __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __r
   }
   const int kbase = kb * kBN;
   const int nt = kbase < st.kend_wave ? (kbase + 32 < st.kend_wave ? 2 : 1) : 0;
-  constexpr bool PRE = dq_prescale<T>();
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     if (t >= nt) break;
-    f32x16 sacc = PRE ? st.neg_lse : zero16(), pacc = st.neg_delta;
+    f32x16 sacc = zero16(), pacc = st.neg_delta;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
       sacc = mfma32(lds_frag16(sK + 32 * t * D + st.koff[s]), st.qf[s], sacc);
@@ -1284,7 +1290,7 @@ __device__ __forceinline__ void dq_block(DqState<T, D>& st, int kb, const T* __r
     if (CAUSAL && kbase + 32 * t == st.qw0) mask_rows_above(sacc, st.lr - 4 * st.g);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = PRE ? fast_exp2(sacc[i]) : fast_exp2(fmaf(sacc[i], st.scale_log2, -st.lse2));
+      const float p = fast_exp2(fmaf(sacc[i], st.scale_log2, -st.lse2));
       sacc[i] = p * pacc[i];  // dS^T = P^T (dP^T - Delta)
     }
 #pragma unroll
@@ -1430,12 +1436,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     if (my_q < L && st.g == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
 #pragma unroll
     for (int i = 0; i < 16; ++i) st.neg_delta[i] = -dl;
-    if constexpr (dq_prescale<T>()) {
-#pragma unroll
-      for (int s = 0; s < D / 16; ++s) st.qf[s] = scale_frag<T>(st.qf[s], scale_log2);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st.neg_lse[i] = -st.lse2;
-    }
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) st.koff[s] = swz_off<D>(st.lr, 2 * s + st.g);
 #pragma unroll

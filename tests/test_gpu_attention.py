@@ -11,17 +11,12 @@ import torch
 
 from oracle.attention import attention_bwd, attention_fwd
 from oracle.schedule import build_schedule, build_schedule_by_sequence
-from parity import UNIT, attn_abs_terms, check_close, cu_of, np64, randn, say
+from parity import UNIT, check_attn, check_close, cu_of, np64, randn, reference_excess, say
 from scree_amd import workloads
 
 pytestmark = pytest.mark.gpu
 
 EDGE_LENGTHS = [1, 63, 64, 65, 127, 128, 129, 255, 300, 2]
-
-
-def _fold(t, kv_heads):
-    n, h, d = t.shape
-    return t.reshape(n, kv_heads, h // kv_heads, d).sum(axis=2)
 
 
 def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True, kv_heads=None):
@@ -39,28 +34,26 @@ def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True, kv_head
     torch.cuda.synchronize()
     q64, k64, v64 = np64(q), np64(k), np64(v)
     ref_o, ref_lse = attention_fwd(q64, k64, v64, off, causal=causal)
-    u = UNIT[dtype]
     bf16 = dtype == torch.bfloat16
     do = randn((n, heads, dim), dtype, seed + 3) if backward else None
     do64 = np64(do) if backward else None
-    terms = None
-    if bf16:  # rounding bounds on the repeated-head problem; dK / dV bounds summed per group
-        g = heads // kv_heads
-        terms = list(attn_abs_terms(q64, np.repeat(k64, g, axis=1), np.repeat(v64, g, axis=1),
-                                    do64, ref_lse, off, causal))
-        if backward:
-            terms[1], terms[3] = _fold(terms[1], kv_heads), _fold(terms[3], kv_heads)
-    check_close("O", np64(out), ref_o, 2e-3,
-                extra=(2 * terms[0] + np.abs(ref_o)) if bf16 else None, unit=u)
+
+    def check(name, got, want, atol):
+        if bf16:  # atol + u|ref| + the reference arithmetic's own excess (tests/parity.py)
+            return check_attn(name, got, want, atol, dtype, e_ref[name])
+        return check_close(name, got, want, atol)
+
+    e_ref = reference_excess(q64, k64, v64, do64, off, causal, dtype) if bf16 else None
+    check("O", np64(out), ref_o, 2e-3)
     check_close("LSE", lse.cpu().numpy().astype(np.float64), ref_lse, 1e-4 + 1e-5 * np.abs(ref_lse).max())
     if not backward:
         return
     dq, dk, dv = varlen_attention_hip_backward(do, q, k, v, out, lse, cu, causal=causal)
     torch.cuda.synchronize()
     rdq, rdk, rdv, _ = attention_bwd(do64, q64, k64, v64, np64(out), ref_lse, off, causal=causal)
-    check_close("dQ", np64(dq), rdq, 5e-3, extra=(2 * terms[2] + np.abs(rdq)) if bf16 else None, unit=u)
-    check_close("dK", np64(dk), rdk, 5e-3, extra=(2 * terms[3] + np.abs(rdk)) if bf16 else None, unit=u)
-    check_close("dV", np64(dv), rdv, 5e-3, extra=(2 * terms[1] + np.abs(rdv)) if bf16 else None, unit=u)
+    check("dQ", np64(dq), rdq, 5e-3)
+    check("dK", np64(dk), rdk, 5e-3)
+    check("dV", np64(dv), rdv, 5e-3)
 
 
 @pytest.mark.parametrize("dim", [32, 64, 128])
@@ -317,23 +310,20 @@ def test_config5_sampled_heads_bf16():
     longest = int(np.argmax(c.lengths))
     picks = sorted({longest, int(np.argmin(c.lengths)), 0, 5})
     heads = [0, 17]
-    u = UNIT[torch.bfloat16]
     for s in picks:
         a, b = int(off[s]), int(off[s + 1])
         say(f"  seq {s} len {b - a} heads {heads}")
-        sl = (slice(a, b), heads)
         sub = lambda t: np64(t[a:b][:, heads])  # noqa: E731
         q64, k64, v64, do64 = sub(q), sub(k), sub(v), sub(do)
         loff = np.array([0, b - a], dtype=np.int32)
         ro, rl = attention_fwd(q64, k64, v64, loff, causal=True, dtype=np.float64)
-        terms = attn_abs_terms(q64, k64, v64, do64, rl, loff, True)
-        check_close("O", sub(out), ro, 2e-3, extra=2 * terms[0] + np.abs(ro), unit=u)
+        e_ref = reference_excess(q64, k64, v64, do64, loff, True, torch.bfloat16)
+        check_attn("O", sub(out), ro, 2e-3, torch.bfloat16, e_ref["O"])
         check_close("LSE", lse[a:b][:, heads].cpu().numpy().astype(np.float64), rl, 1e-4 + 1e-5 * np.abs(rl).max())
         rdq, rdk, rdv, _ = attention_bwd(do64, q64, k64, v64, sub(out), rl, loff, causal=True)
-        check_close("dQ", sub(dq), rdq, 5e-3, extra=2 * terms[2] + np.abs(rdq), unit=u)
-        check_close("dK", sub(dk), rdk, 5e-3, extra=2 * terms[3] + np.abs(rdk), unit=u)
-        check_close("dV", sub(dv), rdv, 5e-3, extra=2 * terms[1] + np.abs(rdv), unit=u)
-        del sl
+        check_attn("dQ", sub(dq), rdq, 5e-3, torch.bfloat16, e_ref["dQ"])
+        check_attn("dK", sub(dk), rdk, 5e-3, torch.bfloat16, e_ref["dK"])
+        check_attn("dV", sub(dv), rdv, 5e-3, torch.bfloat16, e_ref["dV"])
 
 
 @pytest.mark.parametrize("heads,kv_heads", [(8, 8), (16, 4)])

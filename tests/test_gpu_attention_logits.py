@@ -1,0 +1,131 @@
+"""GPU parity of the attention kernels at large logits.
+
+The reference forms every score as an fp32 dot product times ``sm_scale``
+(``src/scree/kernels/triton/varlen_attention.py:128``, ``_backward.py:271``),
+so its arithmetic holds for scores of any size.  N(0,1) inputs keep the
+scaled scores near unit size; here q and k are drawn from N(0, sigma^2)
+(scaled-score standard deviation sigma^2), and a structured case makes later
+keys score far above the first ones, which forces the forward's rare path
+(the reference maximum raised and O and the row sum rescaled when a later
+tile's weights outgrow the first tile's maximum by 2^8).  Each test shows on
+the CPU, from its own inputs, that some row's later keys exceed the maximum
+of its first 32 keys by more than 8 log2 units -- the condition under which
+that path must run -- before comparing with the fp64 oracle.
+
+Bounds: ``atol + u*|ref| + E_ref`` (``tests/parity.py``) for both dtypes.  At
+these logits outputs reach magnitudes (|dK| ~ 16) where half an fp16 ulp
+exceeds the flat 5e-3, and the reference kernels' own fp16 arithmetic departs
+from the fp64 oracle by up to the flat bounds (config 4 at sigma 2: O 1.9e-3,
+dQ 4.9e-3), so both terms are needed; ``E_ref`` is computed on each test's
+own inputs.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import attention_bwd, attention_fwd
+from parity import check_attn, check_close, cu_of, np64, reference_excess, say
+from scree_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+LENGTHS = [1000, 300, 129, 64, 1]
+
+
+def rescale_excess(q, k, off, causal):
+    """max over (row, head) of [max score of keys >= 32] - [max score of keys
+    0..31], in log2 units of the scaled scores (the forward's first tile is
+    keys 0..31 for every row; causal rows see keys up to their own)."""
+    d = q.shape[-1]
+    c = math.log2(math.e) / math.sqrt(d)
+    best = -math.inf
+    for b in range(len(off) - 1):
+        s, e = int(off[b]), int(off[b + 1])
+        if e - s <= 32:
+            continue
+        sc = np.matmul(q[s:e].transpose(1, 0, 2), k[s:e].transpose(1, 2, 0)) * c  # (H, L, L)
+        if causal:
+            sc = np.where(np.triu(np.ones((e - s, e - s), dtype=bool), 1), -np.inf, sc)
+        first = sc[:, :, :32].max(axis=-1)
+        later = sc[:, :, 32:].max(axis=-1)
+        best = max(best, float((later - first).max()))
+    return best
+
+
+def _check(q, k, v, do, off, cu, causal, dtype, min_excess):
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
+
+    q64, k64, v64, do64 = np64(q), np64(k), np64(v), np64(do)
+    excess = rescale_excess(q64, k64, off, causal)
+    say(f"  later-key excess over the first tile's maximum: {excess:.2f} log2 units")
+    assert excess > min_excess, "inputs do not reach the forward's rescale path"
+    out, lse = varlen_attention_hip(q, k, v, cu, causal=causal, return_lse=True)
+    dq, dk, dv = varlen_attention_hip_backward(do, q, k, v, out, lse, cu, causal=causal)
+    torch.cuda.synchronize()
+    ref_o, ref_lse = attention_fwd(q64, k64, v64, off, causal=causal)
+    rdq, rdk, rdv, _ = attention_bwd(do64, q64, k64, v64, np64(out), ref_lse, off, causal=causal)
+    e = reference_excess(q64, k64, v64, do64, off, causal, dtype)
+    check_attn("O", np64(out), ref_o, 2e-3, dtype, e["O"])
+    check_close("LSE", lse.cpu().numpy().astype(np.float64), ref_lse,
+                1e-4 + 1e-5 * np.abs(ref_lse).max())
+    check_attn("dQ", np64(dq), rdq, 5e-3, dtype, e["dQ"])
+    check_attn("dK", np64(dk), rdk, 5e-3, dtype, e["dK"])
+    check_attn("dV", np64(dv), rdv, 5e-3, dtype, e["dV"])
+
+
+def _normal(shape, seed, sigma=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float32) * sigma
+
+
+@pytest.mark.parametrize("sigma", [1.5, 2.0])
+@pytest.mark.parametrize("dim", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_large_logits(sigma, dim, dtype, causal):
+    """q, k ~ N(0, sigma^2): scaled scores with standard deviation sigma^2."""
+    n = sum(LENGTHS)
+    say(f"case: large logits sigma={sigma} lengths={LENGTHS} H=2 D={dim} {dtype} causal={causal}")
+    off, cu = cu_of(LENGTHS)
+    seed = 1000 + dim + int(10 * sigma)
+    q, k = (_normal((n, 2, dim), seed + i, sigma).to(dtype).cuda() for i in range(2))
+    v, do = (_normal((n, 2, dim), seed + i).to(dtype).cuda() for i in (2, 3))
+    _check(q, k, v, do, off, cu, causal, dtype, 8.0)
+
+
+def test_config4_lengths_large_logits_fp16():
+    """The bench's own workload (config 4: 12,160 tokens, 16 heads x 64,
+    causal fp16) with q, k ~ N(0, 4)."""
+    c = workloads.config4()
+    n = c.total
+    say(f"case: config 4 large logits sigma=2 N={n} H={c.heads} D={c.head_dim} fp16 causal")
+    off, cu = cu_of(c.lengths)
+    q, k = (_normal((n, c.heads, c.head_dim), 40 + i, 2.0).half().cuda() for i in range(2))
+    v, do = (_normal((n, c.heads, c.head_dim), 40 + i).half().cuda() for i in (2, 3))
+    _check(q, k, v, do, off, cu, True, torch.float16, 8.0)
+
+
+@pytest.mark.parametrize("dim", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_rising_scores_reach_the_rescale_path(dim, dtype, causal):
+    """Scores that rise along the key axis: q and every key share a direction
+    u (entries +-1), with the keys' share growing linearly with position, so
+    later keys score up to ~14 nats above the first ones (at least 12 log2
+    units above the first tile's maximum)."""
+    lengths = [600, 200, 70]
+    n = sum(lengths)
+    say(f"case: rising scores lengths={lengths} H=2 D={dim} {dtype} causal={causal}")
+    off, cu = cu_of(lengths)
+    g = torch.Generator().manual_seed(77 + dim)
+    u = torch.where(torch.rand(2, dim, generator=g) < 0.5, -1.0, 1.0)  # per head
+    pos = torch.cat([torch.arange(L, dtype=torch.float32) / max(L - 1, 1) for L in lengths])
+    beta = 14.0 / math.sqrt(dim)  # share of u in the last key: q.k / sqrt(D) gains 14
+    q = _normal((n, 2, dim), 5) + u
+    k = _normal((n, 2, dim), 6) + beta * pos[:, None, None] * u
+    v, do = _normal((n, 2, dim), 7), _normal((n, 2, dim), 8)
+    q, k, v, do = (t.to(dtype).cuda() for t in (q, k, v, do))
+    _check(q, k, v, do, off, cu, causal, dtype, 12.0)

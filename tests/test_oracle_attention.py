@@ -288,3 +288,96 @@ def test_gqa_rejects_non_dividing_heads():
     k = np.zeros((3, 3, 8))
     with pytest.raises(ValueError):
         attention_fwd(q, k, k, np.array([0, 3]))
+
+
+# ---- the reference-rounding variants (explain the bf16 error budget) ----
+
+def _torch_rounded(q, k, v, do, off, causal, dt, block=64):
+    """The same arithmetic in torch: P, dS cast with torch's own fp32 ->
+    fp16/bf16 conversion (an implementation of the rounding independent of
+    ``round_bf16``), sums in fp64."""
+    rnd = lambda x: x.float().to(dt).double()  # noqa: E731
+    tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a.transpose(1, 0, 2)))
+                       for a in (q, k, v, do))
+    d = q.shape[-1]
+    o, lse = np.zeros_like(q), np.zeros(q.shape[:2])
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(q), np.zeros_like(q)
+    for b in range(len(off) - 1):
+        s, e = int(off[b]), int(off[b + 1])
+        if e <= s:
+            continue
+        qs, ks, vs, dos = tq[:, s:e], tk[:, s:e], tv[:, s:e], tdo[:, s:e]
+        sc = qs @ ks.transpose(1, 2) / math.sqrt(d)
+        if causal:
+            sc = sc.masked_fill(torch.ones(e - s, e - s, dtype=torch.bool).triu(1), -math.inf)
+        m = torch.full((sc.shape[0], e - s, 1), -math.inf, dtype=torch.float64)
+        l = torch.zeros_like(m)
+        acc = torch.zeros_like(qs)
+        for j in range(0, e - s, block):
+            blk = sc[:, :, j:j + block]
+            mn = torch.maximum(m, blk.amax(-1, keepdim=True))
+            p = torch.exp(blk - mn)
+            a = torch.exp(m - mn)
+            l = a * l + p.sum(-1, keepdim=True)
+            acc = a * acc + rnd(p) @ vs[:, j:j + block]
+            m = mn
+        ob = rnd(acc / l)
+        lb = (m + torch.log(l))[..., 0]
+        o[s:e], lse[s:e] = ob.transpose(0, 1).numpy(), lb.T.numpy()
+        p = torch.exp(sc - lb[..., None])
+        delta = (ob * dos).sum(-1, keepdim=True)
+        ds = rnd(p * (dos @ vs.transpose(1, 2) - delta))
+        dv[s:e] = (rnd(p).transpose(1, 2) @ dos).transpose(0, 1).numpy()
+        dq[s:e] = (ds @ ks / math.sqrt(d)).transpose(0, 1).numpy()
+        dk[s:e] = (ds.transpose(1, 2) @ qs / math.sqrt(d)).transpose(0, 1).numpy()
+    return o, lse, tuple(rnd(torch.from_numpy(g)).numpy() for g in (dq, dk, dv))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_rounded_variant_without_rounding_is_the_oracle(causal):
+    from oracle.attention import attention_bwd_rounded, attention_fwd_rounded
+
+    q, k, v, off = _inputs([70, 1, 130, 64], 2, 16, seed=5)
+    do = np.random.default_rng(6).standard_normal(q.shape)
+    o, lse = attention_fwd(q, k, v, off, causal=causal)
+    o2, lse2 = attention_fwd_rounded(q, k, v, off, causal=causal, operand="float64")
+    np.testing.assert_allclose(o2, o, atol=1e-12)
+    np.testing.assert_allclose(lse2, lse, atol=1e-12)
+    for a, b in zip(attention_bwd(do, q, k, v, o, lse, off, causal=causal),
+                    attention_bwd_rounded(do, q, k, v, o, lse, off, causal=causal, operand="float64")):
+        np.testing.assert_allclose(b, a, atol=1e-12)
+    # grouped K/V heads: the variant expands and folds them like the oracle
+    kg, vg = k[:, :1], v[:, :1]
+    o, lse = attention_fwd(q, kg, vg, off, causal=causal)
+    o2, _ = attention_fwd_rounded(q, kg, vg, off, causal=causal, operand="float64")
+    np.testing.assert_allclose(o2, o, atol=1e-12)
+    for a, b in zip(attention_bwd(do, q, kg, vg, o, lse, off, causal=causal),
+                    attention_bwd_rounded(do, q, kg, vg, o, lse, off, causal=causal, operand="float64")):
+        np.testing.assert_allclose(b, a, atol=1e-12)
+
+
+@pytest.mark.parametrize("operand,dt", [("bfloat16", torch.bfloat16), ("float16", torch.float16)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_rounded_variant_matches_torch_casts(operand, dt, causal):
+    """Rounding placement (P per 64-key block against the running maximum,
+    dS, the stored results) against torch's own casts, and the rounding
+    really applied: the result departs from the exact oracle, by no more
+    than the operand roundings allow."""
+    from oracle.attention import attention_bwd_rounded, attention_fwd_rounded
+
+    q, k, v, off = _inputs([150, 1, 64, 65], 2, 32, seed=9)
+    q, k = 1.5 * q, 1.5 * k  # peaked rows: the running maximum moves between blocks
+    do = np.random.default_rng(10).standard_normal(q.shape)
+    o, lse = attention_fwd_rounded(q, k, v, off, causal=causal, operand=operand)
+    grads = attention_bwd_rounded(do, q, k, v, o, lse, off, causal=causal, operand=operand)
+    to, tl, tg = _torch_rounded(q, k, v, do, off, causal, dt)
+    np.testing.assert_allclose(o, to, atol=1e-12)
+    np.testing.assert_allclose(lse, tl, atol=1e-12)
+    for a, b in zip(grads[:3], tg):
+        np.testing.assert_allclose(a, b, atol=1e-12)
+    exact_o, exact_lse = attention_fwd(q, k, v, off, causal=causal)
+    u = 2.0 ** -8 if operand == "bfloat16" else 2.0 ** -11
+    err = np.abs(o - exact_o)
+    assert err.max() > 0.1 * u
+    assert (err <= u * (np.abs(v).max() + np.abs(exact_o)) + 1e-12).all()
+    np.testing.assert_allclose(lse, exact_lse, atol=1e-12)  # the row sum is unrounded
