@@ -658,10 +658,26 @@ constexpr int acc_row0(int i) { return 8 * (i >> 2) + (i & 3); }
 
 // Mask (to -inf) the elements of a 32x32 tile whose row exceeds `rel`:
 // element i is row acc_row0(i) + 4g, so the test is acc_row0(i) > rel - 4g.
+// Callers mask only the (rare) diagonal tile, under a branch.  The empty
+// volatile asm cannot be speculated, so the compiler keeps that branch:
+// without it, it turned the masking into 16 v_cndmask executed on every
+// tile (32 in the dK/dV pass), their 16 lane masks held in registers across
+// the block loop.  The forward (OPAQUE = false) masks only in the blocks of
+// its peeled diagonal loop, where the plain form needs no extra register.
+template <bool OPAQUE = true>
 __device__ __forceinline__ void mask_rows_above(f32x16& c, int rel_minus_4g) {
+  if (OPAQUE) asm volatile("" : "+v"(rel_minus_4g));
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     if (acc_row0(i) > rel_minus_4g) c[i] = kNegInf;
+}
+// The converse: mask the elements whose row is below `rel` (acc_row0(i) <
+// rel - 4g).
+__device__ __forceinline__ void mask_rows_below(f32x16& c, int rel_minus_4g) {
+  asm volatile("" : "+v"(rel_minus_4g));
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (acc_row0(i) < rel_minus_4g) c[i] = kNegInf;
 }
 
 // Wave index as a scalar, so per-wave tile bounds are uniform branches.
@@ -971,9 +987,9 @@ __device__ __forceinline__ float tile_max_fresh(const f32x16& s) {
 template <typename T, int D, bool CAUSAL>
 __device__ __forceinline__ void fwd_mask(const FwdState<T, D>& st, f32x16& s, int tbase) {
   if (CAUSAL) {
-    if (tbase == st.qw0) mask_rows_above(s, st.lr - 4 * st.g);  // the diagonal tile
+    if (tbase == st.qw0) mask_rows_above<false>(s, st.lr - 4 * st.g);  // the diagonal tile
   } else if (tbase + 32 > st.L) {
-    mask_rows_above(s, st.L - 1 - tbase - 4 * st.g);
+    mask_rows_above<false>(s, st.L - 1 - tbase - 4 * st.g);
   }
 }
 
@@ -1339,19 +1355,22 @@ __device__ __forceinline__ void dq_run(DqState<T, D>& st, T* __restrict__ A, T* 
     barrier_vm<NL>();
   else
     barrier_vm<0>();
+  auto block = [&](int kb, const T* __restrict__ cur, T* __restrict__ nxt) {
+    dq_block<T, D, CAUSAL, three ? 2 : 1>(st, kb, cur, nxt);
+  };
   if constexpr (three) {
     for (int kb = 0; kb < st.nkb; kb += 3) {
-      dq_block<T, D, CAUSAL, 2>(st, kb, A, C);
+      block(kb, A, C);
       if (kb + 1 >= st.nkb) break;
-      dq_block<T, D, CAUSAL, 2>(st, kb + 1, B, A);
+      block(kb + 1, B, A);
       if (kb + 2 >= st.nkb) break;
-      dq_block<T, D, CAUSAL, 2>(st, kb + 2, C, B);
+      block(kb + 2, C, B);
     }
   } else {
     for (int kb = 0; kb < st.nkb; kb += 2) {
-      dq_block<T, D, CAUSAL, 1>(st, kb, A, B);
+      block(kb, A, B);
       if (kb + 1 >= st.nkb) break;
-      dq_block<T, D, CAUSAL, 1>(st, kb + 1, B, A);
+      block(kb + 1, B, A);
     }
   }
 }
@@ -1558,6 +1577,9 @@ __device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __
         sacc = mfma32(lds_frag16(sQ + 32 * u * D + st.qoff[s]), kfr, sacc);
         pacc = mfma32(lds_frag16(sO + 32 * u * D + st.qoff[s]), st.vf[s], pacc);
       }
+      // diagonal tile: queries before the key contribute nothing (their
+      // scores go to -inf, so P = 0 and dS = 0 * (dP - Delta) = 0)
+      if (CAUSAL && qt0 == st.kw0) mask_rows_below(sacc, st.lr - 4 * st.g);
       f32x16 pv;
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
@@ -1569,16 +1591,6 @@ __device__ __forceinline__ void dkv_block(DkvState<T, D>& st, int b, const T* __
           const float p = fast_exp2(fmaf(sacc[i], st.scale_log2, -la[e]));
           pv[i] = p;
           sacc[i] = p * pacc[i];  // dS = P (dP - Delta)
-        }
-      }
-      if (CAUSAL && qt0 == st.kw0) {
-        // diagonal tile: queries before the key contribute nothing
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if (acc_row0(i) < st.lr - 4 * st.g) {
-            pv[i] = 0.f;
-            sacc[i] = 0.f;
-          }
         }
       }
 #pragma unroll
