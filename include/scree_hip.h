@@ -23,7 +23,9 @@
  * Layouts
  *   - Attention tensors are (total_tokens, heads, head_dim) with the
  *     head_dim axis contiguous; row and head strides are given in elements
- *     and must keep every row 16-byte aligned.  lse and delta are contiguous
+ *     and must keep every row 16-byte aligned.  head_dim is 16, 32, 64, 128
+ *     or 256 (SCREE_ERR_UNSUPPORTED otherwise); the reference's launcher
+ *     takes any power of two (src/scree/kernels/triton/varlen_attention.py:217).  lse and delta are contiguous
  *     (total_tokens, heads) fp32.
  *   - Norm tensors are contiguous (rows, dim); rstd / mean are (rows) fp32.
  */
@@ -77,11 +79,15 @@ size_t scree_attn_workspace_bytes(int batch, int64_t total_tokens, int head_dim)
 
 /* 1 when scree_attn_fwd / scree_attn_fwd_gqa read a work list that
  * scree_attn_schedule must write first; 0 when the forward derives every
- * workgroup's item from cu_seqlens itself and leaves the work lists in its
- * workspace, exactly as scree_attn_schedule writes them, so a forward
- * followed by backward calls on the same workspace needs no schedule call.
+ * workgroup's item from cu_seqlens itself and writes the header and the
+ * work-order list into its workspace as scree_attn_schedule writes them, so
+ * the backward calls of the same problem (same cu_seqlens, total_tokens,
+ * heads, head_dim, causal) on that workspace need no schedule call.  The
+ * sequence-major list, which launches of many workgroups per XCD read, is
+ * left as it was: any other call on the workspace -- a forward or backward
+ * of another problem, e.g. with more heads -- needs scree_attn_schedule.
  * The forward derives for at most 64 sequences in a launch of at most 2048
- * workgroups at head_dim <= 64, 1024 at head_dim 128, i.e.
+ * workgroups at head_dim <= 64, 1024 at head_dim 128, 512 at 256, i.e.
  * (ceil(total_tokens / 128) + batch) * heads within that bound; past it the
  * derivation (~150 instructions per workgroup) costs more than the scheduler
  * launch.  Backward calls that no forward on their workspace precedes always
@@ -119,8 +125,8 @@ int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t total_toke
  * lse = natural-log logsumexp of the scaled scores per (token, head).
  * strides[8] = {q_row, q_head, k_row, k_head, v_row, v_head, o_row, o_head}.
  * When scree_attn_needs_schedule returns 0 it derives its work items from
- * cu_seqlens and writes the work lists into `workspace`; otherwise it reads
- * the lists scree_attn_schedule wrote there.
+ * cu_seqlens and writes the header and work-order list into `workspace`;
+ * otherwise it reads the lists scree_attn_schedule wrote there.
  * Replaces _varlen_attn_fwd_kernel + launcher
  * (src/scree/kernels/triton/varlen_attention.py:35-268). */
 int scree_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,

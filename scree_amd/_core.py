@@ -65,6 +65,18 @@ class Array:
                 f"values.shape[ragged_dim={self.ragged_dim}] ({ragged_size})"
             )
 
+    @classmethod
+    def _trusted(cls, values: Any, offsets: Any, ragged_dim: int = 0) -> "Array":
+        """An Array whose invariants the caller already holds -- a kernel
+        output that reuses the validated offsets of its input -- built
+        without ``__post_init__``'s reads of ``offsets[0]`` and
+        ``offsets[-1]``, which are host synchronisations for device offsets."""
+        obj = object.__new__(cls)
+        object.__setattr__(obj, "values", values)
+        object.__setattr__(obj, "offsets", offsets)
+        object.__setattr__(obj, "ragged_dim", ragged_dim)
+        return obj
+
     @property
     def batch_size(self) -> int:
         return len(self.offsets) - 1

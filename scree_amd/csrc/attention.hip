@@ -49,9 +49,11 @@ constexpr float kNegInf = -__builtin_inff();
 // int4 items[Tmax] = {seq, blk, start, len}: longest-work-first, then the same
 // items sequence by sequence (attn_schedule_kernel).  start/len are the sequence's offsets clamped to
 // [0, total_tokens], so attention kernels never index outside the tensors
-// even for malformed offsets; if those would make T exceed Tmax the
+// even for malformed offsets.  If any offset decreases (overlapping or
+// negative-length sequences), or the offsets would make T exceed Tmax, the
 // scheduler publishes T = 0 (no work) and header[1] = -1, and the attention
-// kernels then fill their outputs with NaN (poison_rows).
+// kernels then fill their outputs with NaN (poison_rows): the device-side
+// check that lets callers skip a host read of the offsets.
 constexpr size_t kHeaderBytes = 16;
 
 inline int64_t tmax_for(int batch, int64_t total) { return (total + kBM - 1) / kBM + batch; }
@@ -129,11 +131,12 @@ __global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __re
   __shared__ int s_nat_scan[kMaxBatch + 1];
   __shared__ int s_cls[kMaxClass + 2];
   __shared__ int s_wtot[64];
-  __shared__ int s_cmax;
+  __shared__ int s_cmax, s_bad;
   const int tid = threadIdx.x, nt = blockDim.x;
-  if (tid == 0) s_cmax = 0;
+  if (tid == 0) s_cmax = s_bad = 0;
   __syncthreads();
   for (int s = tid; s < batch; s += nt) {
+    if (cu[s + 1] < cu[s]) s_bad = 1;  // decreasing offsets: the schedule fails
     const int a = min(max(cu[s], 0), total_tokens);
     const int b = min(max(cu[s + 1], a), total_tokens);
     const int len = b - a;
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(1024) void attn_schedule_kernel(const int32_t* __re
   }
   __syncthreads();
   // Emit: natural item index i -> (seq, blk) by binary search, then place.
-  const bool fits = total <= tmax;
+  const bool fits = total <= tmax && !s_bad;
   for (int i = tid; fits && i < total; i += nt) {
     int lo = 0, hi = batch - 1;  // find s with nat[s] <= i < nat[s+1]
     while (lo < hi) {
@@ -280,6 +283,7 @@ __device__ __forceinline__ int first_lane(bool pred) {
 struct WaveSched {
   int start, len, nb;  // this lane's sequence: clamped start, length, row blocks
   int total, cmax;     // item count and largest nblk (wave-uniform)
+  bool bad;            // some offset decreases (wave-uniform): the schedule fails
 };
 
 // Offsets are clamped as in attn_schedule_kernel; lanes >= batch hold empty
@@ -289,10 +293,14 @@ __device__ __forceinline__ WaveSched wave_sched(const int32_t* __restrict__ cu, 
   const int lane = threadIdx.x & (kWave - 1);
   WaveSched w;
   int a = 0, b = 0;
+  bool dec = false;
   if (lane < batch) {
-    a = min(max(cu[lane], 0), total_tokens);
-    b = min(max(cu[lane + 1], a), total_tokens);
+    const int c0 = cu[lane], c1 = cu[lane + 1];
+    dec = c1 < c0;
+    a = min(max(c0, 0), total_tokens);
+    b = min(max(c1, a), total_tokens);
   }
+  w.bad = __ballot(dec) != 0;
   w.start = a;
   w.len = b - a;
   w.nb = (w.len + kBM - 1) / kBM;
@@ -318,7 +326,7 @@ __device__ __forceinline__ int lane_of_rank(const WaveSched& w, int r, int lo) {
   int hi = w.cmax;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (__popcll(__ballot(w.nb >= mid)) > r)
+    if ((int)__popcll(__ballot(w.nb >= mid)) > r)
       lo = mid;
     else
       hi = mid - 1;
@@ -378,7 +386,7 @@ __global__ __launch_bounds__(256) void attn_wave_schedule_kernel(const int32_t* 
                                                                  int32_t* __restrict__ header,
                                                                  int4* __restrict__ items) {
   const WaveSched w = wave_sched(cu, batch, total_tokens);
-  const bool fits = w.total <= tmax;
+  const bool fits = w.total <= tmax && !w.bad;
   const int p = blockIdx.x * (blockDim.x / kWave) + (int)(threadIdx.x / kWave);
   if (fits && p < w.total) {
     const int4 a = wave_item(w, batch, causal != 0, false, p);
@@ -435,10 +443,10 @@ template <bool MAY_DERIVE>
 __device__ __forceinline__ ItemView item_view(const ItemSource& src, int tmax) {
   const int listed_count = src.header[0], listed_batch = src.header[1];
   ItemView v;
-  v.w = WaveSched{0, 0, 0, 0, 0};
+  v.w = WaveSched{0, 0, 0, 0, 0, false};
   if (MAY_DERIVE && src.derive) v.w = wave_sched(src.cu, src.batch, src.total_tokens);
   const bool derive = MAY_DERIVE && src.derive;
-  v.failed = derive ? v.w.total > tmax : listed_batch < 0;
+  v.failed = derive ? (v.w.total > tmax || v.w.bad) : listed_batch < 0;
   v.count = derive ? (v.failed ? 0 : v.w.total) : min(max(listed_count, 0), tmax);
   return v;
 }
@@ -487,15 +495,16 @@ __global__ __launch_bounds__(1024) void attn_big_schedule_kernel(
     const int32_t* __restrict__ cu, int batch, int total_tokens, int causal, int tmax,
     int32_t* __restrict__ header, int4* __restrict__ items, int32_t* __restrict__ prefix) {
   __shared__ int s_wtot[16];
-  __shared__ int s_run;
+  __shared__ int s_run, s_bad;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int nw = blockDim.x / kWave;
-  if (tid == 0) s_run = 0;
+  if (tid == 0) s_run = s_bad = 0;
   __syncthreads();
   for (int c0 = 0; c0 < batch; c0 += blockDim.x) {  // exclusive scan of nblk, chunk by chunk
     const int s = c0 + tid;
     int nb = 0;
     if (s < batch) {
+      if (cu[s + 1] < cu[s]) s_bad = 1;  // decreasing offsets: the schedule fails
       const int a = min(max(cu[s], 0), total_tokens);
       const int b = min(max(cu[s + 1], a), total_tokens);
       nb = (b - a + kBM - 1) / kBM;
@@ -518,7 +527,7 @@ __global__ __launch_bounds__(1024) void attn_big_schedule_kernel(
   if (tid == 0) prefix[batch] = total;
   __threadfence();  // the prefix sums, written by every thread, are read by any
   __syncthreads();
-  const bool fits = total <= tmax;
+  const bool fits = total <= tmax && !s_bad;
   for (int i = tid; fits && i < total; i += blockDim.x) {
     int lo = 0, hi = batch - 1;  // the last sequence s with prefix[s] <= i (skips empty ones)
     while (lo < hi) {
@@ -577,6 +586,19 @@ template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 gmem_frag16(const T* p) {
   return __builtin_bit_cast(typename VecT<T>::x8, ld16(p));
 }
+// head_dim 16 runs the 32-column kernels on rows padded with zero columns:
+// they add nothing to any dot product, and the padded outputs are not stored.
+// Only the 32-column kernels can see a row narrower than their D (dcols).
+template <int D>
+__device__ __forceinline__ bool col_live(int c0, int dcols) {
+  return D > 32 || c0 < dcols;
+}
+// Columns [c0, c0 + 8) of a row that holds `dcols` columns; zeros past them.
+template <int D, typename T>
+__device__ __forceinline__ typename VecT<T>::x8 gmem_frag16_cols(const T* row, int c0, int dcols) {
+  if (col_live<D>(c0, dcols)) return gmem_frag16(row + c0);
+  return __builtin_bit_cast(typename VecT<T>::x8, make_uint4(0u, 0u, 0u, 0u));
+}
 // Elements e0..e0+7 of a 16-float accumulator, rounded to T, as an operand.
 template <typename T>
 __device__ __forceinline__ typename VecT<T>::x8 pack_frag(const f32x16& c, int e0) {
@@ -605,7 +627,8 @@ __device__ __forceinline__ void store_row_slice(T* row_ptr, int d0, int g, const
 // lane's `mul`) into a wave-private LDS area of 32 rows x (D + 8) elements
 // (the pad spreads the rows over the banks), then reads it back so that lane
 // l holds 16-byte chunk l % CPR of row l / CPR (+ 64 / CPR per round), and
-// CPR lanes store one contiguous row.  Rows >= nrows are not stored.  LDS
+// CPR lanes store one contiguous row.  Rows >= nrows and columns >= dcols
+// (head_dim 16 in the 32-column kernels) are not stored.  LDS
 // accesses of one wave are processed in order, so the read-back sees the
 // writes without a workgroup barrier; the caller guarantees no other wave
 // uses `stage` meanwhile.
@@ -617,7 +640,7 @@ constexpr int stage_elems() {
 template <typename T, int D>
 __device__ __forceinline__ void store_rows_staged(T* __restrict__ stage, const f32x16 (&acc)[D / 32],
                                                   float mul, T* __restrict__ dst, int64_t row_stride,
-                                                  int nrows, int lr, int g, int lane) {
+                                                  int nrows, int dcols, int lr, int g, int lane) {
   constexpr int SD = D + kStagePad;
   constexpr int CPR = D / 8;       // 16-byte chunks per row
   constexpr int RPR = 64 / CPR;    // rows per read round
@@ -637,7 +660,8 @@ __device__ __forceinline__ void store_rows_staged(T* __restrict__ stage, const f
   for (int j = 0; j < 32 / RPR; ++j) {
     const int r = lane / CPR + RPR * j;
     const uint4 v = *reinterpret_cast<const uint4*>(stage + r * SD + 8 * c);
-    if (r < nrows) *reinterpret_cast<uint4*>(dst + (int64_t)r * row_stride + 8 * c) = v;
+    if (r < nrows && col_live<D>(8 * c, dcols))
+      *reinterpret_cast<uint4*>(dst + (int64_t)r * row_stride + 8 * c) = v;
   }
 }
 
@@ -692,7 +716,7 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // issuing wave's vmcnt has counted it.
 template <int N>
 __device__ __forceinline__ void barrier_vm() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  static_assert(N >= 0 && N < 64, "vmcnt immediate (6 bits on gfx9)");
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
@@ -741,9 +765,9 @@ __device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, i
   return true;
 }
 
-// The scheduler publishes header[1] = -1 when the offsets describe more work
-// than the host bound allows (possible only for offsets that decrease, i.e.
-// overlapping sequences).  Every kernel then fills its outputs with NaN, block
+// The scheduler publishes header[1] = -1 when some offset decreases (which is
+// also the only way the offsets can describe more work than the host bound
+// allows).  Every kernel then fills its outputs with NaN, block
 // b taking token rows b, b + grid, ..., instead of leaving them unwritten.
 template <typename T>
 __device__ __forceinline__ void poison_rows(T* __restrict__ p, Strides s, int total, int heads, int d) {
@@ -760,12 +784,27 @@ __device__ __forceinline__ void poison_stats(float* __restrict__ p, int total, i
 // The forward keeps a reference maximum m per softmax row and forms weights
 // p = 2^(s*c - m*c) without first taking each tile's maximum: a lane checks
 // the sum of its 16 weights of the tile instead.  The weights are >= 0, so a
-// sum <= kSumLimit bounds every weight by 2^8, which fp32 sums and fp16/bf16
-// operands hold with the same relative precision as values <= 1.  Only when
-// some lane's sum exceeds it (or is NaN) does the wave take the tile maximum,
-// raise m, rescale O and the row sum, and form the weights again -- rarely:
-// a wave's first tile sets m from the tile itself (fwd_first_weights).
-constexpr float kSumLimit = 256.0f;
+// sum <= sum_limit bounds every weight by it, and fp32 sums and fp16/bf16
+// operands hold such weights with the same relative precision as values
+// <= 1.  Only when some lane's sum exceeds it (or is NaN) does the wave take
+// the tile maximum, raise m, rescale O and the row sum, and form the weights
+// again -- rarely: a wave's first tile sets m from the tile itself
+// (fwd_first_weights).
+//
+// What the limit trades is how often a row's largest weights are exact: a
+// tile that raises m gives its largest weight exactly 1, as the reference's
+// per-block running maximum gives every block's (triton/varlen_attention.py
+// :137-142), while weights under a lagging m sit anywhere up to the limit and
+// carry their operand rounding into O.  fp16 rounds finely enough for 2^8.
+// bf16 rounds 8x coarser: with 2^8 its O departed from the fp64 oracle by up
+// to 2.2x what the reference kernels' own bf16 rounding gives on the same
+// inputs at q, k ~ N(0, 4) (a CPU emulation of both over 6 seeds x 3
+// head_dims); 2^3 keeps it within 1.5x, still rarely taking the rescale on
+// unit-variance scores (the first tile's maximum is then ~2 sigma high).
+template <typename T>
+constexpr float sum_limit() {
+  return std::is_same<T, bf16>::value ? 8.0f : 256.0f;
+}
 
 // ------------------------------------------------------- tile staging
 // Direct-to-LDS tiles.  A ROWS x D tile of one head is copied from HBM into
@@ -808,13 +847,18 @@ struct DmaTile {
   static constexpr int PER_WAVE = INSTR / 4;
   uint32_t voff[PER_WAVE];
 
-  __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
+  // Chunks past the row's `dcols` columns (head_dim 16 in the 32-column
+  // kernels) get an offset past every buffer's record count: the hardware
+  // returns zeros for them, as for rows past the sequence.
+  __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane, int dcols) {
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
       const int q = i * 4 + wave;
       const int r = q * RPI + lane / CPR;
       const int c = (lane % CPR) ^ swz<D>(r);
-      voff[i] = (uint32_t)(((int64_t)r * row_stride + c * 8) * (int64_t)sizeof(T));
+      voff[i] = col_live<D>(8 * c, dcols)
+                    ? (uint32_t)(((int64_t)r * row_stride + c * 8) * (int64_t)sizeof(T))
+                    : 0xFFFFFFF0u;
     }
   }
   // rows [row0, row0 + ROWS) of a sequence starting at `base` into `lds`
@@ -879,13 +923,14 @@ __device__ __forceinline__ float halves_sum(float x) {
 // bf16 forward: O is normalised by the sum of the weights as rounded into the
 // P operand, while the LSE keeps the sum of the unrounded weights (as the
 // reference's l, triton/varlen_attention.py:138).  The weights here are taken
-// against a reference maximum that may lag the row's true maximum by up to
-// 2^8 (kSumLimit), so a row's dominant weight is an arbitrary value in
-// (1, 256] whose bf16 rounding (2^-9 relative) would otherwise pass straight
-// into O; the reference's dominant weight is exp(0) = 1, exact.  Dividing by
-// the operand sum makes O a convex combination of V rows with the rounded
-// weights, in which a dominant weight's rounding cancels.  (fp16 rounds 8x
-// finer; its budget holds without the second sum.)  Cost: 8 v_dot2 per tile.
+// against a reference maximum that may lag the row's true maximum (by up to
+// sum_limit), so a row's dominant weight can be an arbitrary value above 1
+// whose bf16 rounding (2^-9 relative) would otherwise pass straight into O;
+// the reference's dominant weight is exp(0) = 1, exact.  Dividing by the
+// operand sum makes O a convex combination of V rows with the rounded
+// weights, in which a lone dominant weight's rounding cancels.  (fp16 rounds
+// 8x finer; its budget holds without the second sum.)  Cost: 8 v_dot2 per
+// tile.
 template <typename T>
 constexpr bool fwd_operand_sum() {
   return std::is_same<T, bf16>::value;
@@ -1001,7 +1046,7 @@ __device__ __forceinline__ float fwd_weights(const FwdState<T, D>& st, const f32
   return tile_sum(p);
 }
 
-// The rare path: some lane's weights summed past kSumLimit (or to NaN).
+// The rare path: some lane's weights summed past sum_limit (or to NaN).
 // Raise the reference maximum to the tile's, rescale O and the row sum, and
 // form the tile's weights again.
 template <typename T, int D>
@@ -1079,12 +1124,12 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
         ls0 = fwd_first_weights(st, s0, p0);
       } else {
         ls0 = fwd_weights(st, s0, p0);
-        if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+        if (__any(!(ls0 <= sum_limit<T>()))) fwd_rescale(st, s0, p0, ls0);
       }
       st.l_run += ls0;
       fwd_pv(st, p0, sV);
       float ls1 = fwd_weights(st, s1, p1);
-      if (__any(!(ls1 <= kSumLimit))) fwd_rescale(st, s1, p1, ls1);
+      if (__any(!(ls1 <= sum_limit<T>()))) fwd_rescale(st, s1, p1, ls1);
       st.l_run += ls1;
       fwd_pv(st, p1, sV + 32 * D);
     } else {
@@ -1099,14 +1144,14 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
         ls0 = fwd_first_weights(st, s0, p0);
       } else {
         ls0 = fwd_weights(st, s0, p0);
-        if (__any(!(ls0 <= kSumLimit))) fwd_rescale(st, s0, p0, ls0);
+        if (__any(!(ls0 <= sum_limit<T>()))) fwd_rescale(st, s0, p0, ls0);
       }
       st.l_run += ls0;
       fwd_pv(st, p0, sV);
       if (nt > 1) {
         fwd_mask<T, D, CAUSAL>(st, s1, kbase + 32);
         float ls1 = fwd_weights(st, s1, p1);
-        if (__any(!(ls1 <= kSumLimit))) fwd_rescale(st, s1, p1, ls1);
+        if (__any(!(ls1 <= sum_limit<T>()))) fwd_rescale(st, s1, p1, ls1);
         st.l_run += ls1;
         fwd_pv(st, p1, sV + 32 * D);
       }
@@ -1122,14 +1167,15 @@ __device__ __forceinline__ void fwd_block(FwdState<T, D>& st, int kb, const T* _
 // waves, for the non-causal form at 64).
 template <int D, bool CAUSAL>
 constexpr int attn_fwd_waves() {
-  return CAUSAL && D <= 64 ? 4 : 2;
+  return D >= 256 ? 1 : CAUSAL && D <= 64 ? 4 : 2;
 }
 
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, ItemSource src, int tmax, int head_major, int heads, int group,
-    Strides sq, Strides sk, Strides sv, Strides so, float scale, float scale_log2, int total) {
+    Strides sq, Strides sk, Strides sv, Strides so, float scale, float scale_log2, int total,
+    int dcols) {
   constexpr int TILE = kBN * D;  // elements per K or V tile
   constexpr int BUF = 2 * TILE;  // one buffer: K tile then V tile
   __shared__ __align__(16) T smem[2 * BUF];
@@ -1138,7 +1184,7 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
   const ItemView iv = item_view<true>(src, tmax);
   if (iv.failed) {
     publish_header(src, iv, CAUSAL ? 1 : 0);
-    poison_rows(o, so, total, heads, D);
+    poison_rows(o, so, total, heads, dcols);
     poison_stats(lse, total, heads);
     return;
   }
@@ -1171,15 +1217,15 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
 
   T* bufA = smem;
   T* bufB = smem + BUF;
-  st.dK.init(sk.row, st.wave, lane);
-  st.dV.init(sv.row, st.wave, lane);
+  st.dK.init(sk.row, st.wave, lane, dcols);
+  st.dV.init(sv.row, st.wave, lane, dcols);
   st.dK.load(bufA, st.kh, sk.row, 0, L, st.wave);
   st.dV.load(bufA + TILE, st.vh, sv.row, 0, L, st.wave);
 
   {  // rows past L read row L-1: their results are never stored
     const T* qrow = q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
+    for (int s = 0; s < D / 16; ++s) st.qf[s] = gmem_frag16_cols<D>(qrow, 16 * s + 8 * st.g, dcols);
     // Materialize the fragments before the barrier (the compiler would sink
     // the loads into the block loop, whose counter waits would then also wait
     // out the freshly issued DMA).
@@ -1235,7 +1281,7 @@ __global__ __launch_bounds__(kThreads, (attn_fwd_waves<D, CAUSAL>())) void attn_
     const float inv_l = 1.0f / (fwd_operand_sum<T>() ? halves_sum(st.l_op) : l_tot);
     store_rows_staged<T, D>(smem + st.wave * stage_elems<D>(), st.oacc, inv_l,
                             o + (int64_t)(start + st.qw0) * so.row + (int64_t)h * so.head, so.row,
-                            min(32, L - st.qw0), st.lr, st.g, lane);
+                            min(32, L - st.qw0), dcols, st.lr, st.g, lane);
     if (st.g == 0 && my_q < L)
       lse[(int64_t)(start + my_q) * heads + h] = st.m_run * scale + logf(l_tot);
   }
@@ -1376,13 +1422,13 @@ __device__ __forceinline__ void dq_run(DqState<T, D>& st, T* __restrict__ A, T* 
 }
 
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
+__global__ __launch_bounds__(kThreads, D >= 256 ? 1 : 2) void attn_bwd_dq_kernel(
     const T* __restrict__ dout, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ o, const float* __restrict__ lse,
     float* __restrict__ delta, T* __restrict__ dq, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sdo,
     Strides sq, Strides sk, Strides sv, Strides so, Strides sdq, float scale, float scale_log2,
-    int total) {
+    int total, int dcols) {
   typedef typename VecT<T>::x8 x8;
   constexpr int TILE = kBN * D;
   constexpr int BUF = 2 * TILE;  // K tile then V tile
@@ -1391,7 +1437,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
 
   const ItemView iv = item_view<false>(src, tmax);
   if (iv.failed) {
-    poison_rows(dq, sdq, total, heads, D);
+    poison_rows(dq, sdq, total, heads, dcols);
     poison_stats(delta, total, heads);
     return;
   }
@@ -1420,8 +1466,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   st.nkb = (kend_wg + kBN - 1) / kBN;
   st.kend_wave = wave_live ? (CAUSAL ? min(L, st.qw0 + 32) : L) : 0;
 
-  st.dK.init(sk.row, st.wave, lane);
-  st.dV.init(sv.row, st.wave, lane);
+  st.dK.init(sk.row, st.wave, lane, dcols);
+  st.dV.init(sv.row, st.wave, lane, dcols);
 
   // This wave's query rows (issued before the first K/V blocks), then Delta
   // and the fragment offsets, set up while those blocks are in flight.  Rows
@@ -1435,9 +1481,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const T* orow = o + tok * so.row + (int64_t)h * so.head;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
-      st.qf[s] = gmem_frag16(qrow + 16 * s + 8 * st.g);
-      st.df[s] = gmem_frag16(drow + 16 * s + 8 * st.g);
-      of[s] = gmem_frag16(orow + 16 * s + 8 * st.g);
+      st.qf[s] = gmem_frag16_cols<D>(qrow, 16 * s + 8 * st.g, dcols);
+      st.df[s] = gmem_frag16_cols<D>(drow, 16 * s + 8 * st.g, dcols);
+      of[s] = gmem_frag16_cols<D>(orow, 16 * s + 8 * st.g, dcols);
     }
     lse_raw = lse[tok * heads + h];
   };
@@ -1468,7 +1514,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
   if (wave_live)  // the last block's barrier freed the tile buffers: stage dQ there
     store_rows_staged<T, D>(smem + st.wave * stage_elems<D>(), st.dqacc, scale,
                             dq + (int64_t)(start + st.qw0) * sdq.row + (int64_t)h * sdq.head,
-                            sdq.row, min(32, L - st.qw0), st.lr, st.g, lane);
+                            sdq.row, min(32, L - st.qw0), dcols, st.lr, st.g, lane);
 }
 
 // ---------------------------------------------------- backward: dK and dV
@@ -1650,7 +1696,8 @@ constexpr int kRedRows = 16;
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dkv_reduce_kernel(
     const float* __restrict__ partial, ItemSource src, int tmax, int causal, int kv_heads,
-    int gsplit, T* __restrict__ dk, T* __restrict__ dv, Strides sdk, Strides sdv, float scale) {
+    int gsplit, T* __restrict__ dk, T* __restrict__ dv, Strides sdk, Strides sdv, float scale,
+    int dcols) {
   constexpr int CHUNKS = kBM / kRedRows;
   const int slot = blockIdx.x / CHUNKS, chunk = blockIdx.x % CHUNKS;
   const int item = slot / kv_heads, hk = slot % kv_heads;
@@ -1665,7 +1712,7 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(
   const float* base = partial + (int64_t)slot * gsplit * part_floats;
   for (int idx = threadIdx.x; idx < kRedRows * C4; idx += blockDim.x) {
     const int r = chunk * kRedRows + idx / C4, c = 4 * (idx % C4);
-    if (k0 + r >= L) continue;
+    if (k0 + r >= L || !col_live<D>(c, dcols)) continue;
 #pragma unroll
     for (int kind = 0; kind < 2; ++kind) {
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1688,7 +1735,7 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(
 // two otherwise.
 template <int D, bool CAUSAL>
 constexpr int dkv_waves() {
-  return D <= 32 || (D == 64 && CAUSAL) ? 3 : 2;
+  return D >= 256 ? 1 : D <= 32 || (D == 64 && CAUSAL) ? 3 : 2;
 }
 
 template <typename T, int D, bool CAUSAL, bool SPLIT, bool REV>
@@ -1698,7 +1745,7 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
     T* __restrict__ dk, T* __restrict__ dv, ItemSource src, int tmax, int head_major,
     int kv_heads, int group,
     Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk, Strides sdv, float scale,
-    float scale_log2, int gsplit, float* __restrict__ partial, int total) {
+    float scale_log2, int gsplit, float* __restrict__ partial, int total, int dcols) {
   constexpr int BQ = dkv_bq<D>();
   constexpr int TILE = BQ * D;
   constexpr int BUF = 2 * TILE;  // Q tile then dO tile
@@ -1719,8 +1766,8 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   // adds them up after the pass.
   const ItemView iv = item_view<false>(src, tmax);
   if (iv.failed) {
-    poison_rows(dk, sdk, total, kv_heads, D);
-    poison_rows(dv, sdv, total, kv_heads, D);
+    poison_rows(dk, sdk, total, kv_heads, dcols);
+    poison_rows(dv, sdv, total, kv_heads, dcols);
     return;
   }
   int item, hv;
@@ -1759,8 +1806,8 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
 
   T* bufA = smem;
   T* bufB = smem + BUF;
-  st.dQ.init(sq.row, st.wave, lane);
-  st.dO.init(sdo.row, st.wave, lane);
+  st.dQ.init(sq.row, st.wave, lane, dcols);
+  st.dO.init(sdo.row, st.wave, lane, dcols);
   // Query head h: point the state at it and stage its first block.
   auto start_head = [&](int h) {
     st.qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
@@ -1789,10 +1836,10 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
     for (int s = 0; s < D / 16; ++s) {
       if constexpr (dkv_k_lds<D>())
         *reinterpret_cast<uint4*>(kl + st.qoff[s]) =
-            __builtin_bit_cast(uint4, gmem_frag16(krow + 16 * s + 8 * st.g));
+            __builtin_bit_cast(uint4, gmem_frag16_cols<D>(krow, 16 * s + 8 * st.g, dcols));
       else
-        st.kf[s] = gmem_frag16(krow + 16 * s + 8 * st.g);
-      st.vf[s] = gmem_frag16(vrow + 16 * s + 8 * st.g);
+        st.kf[s] = gmem_frag16_cols<D>(krow, 16 * s + 8 * st.g, dcols);
+      st.vf[s] = gmem_frag16_cols<D>(vrow, 16 * s + 8 * st.g, dcols);
     }
     // Materialize the fragments here, before the barrier: left to itself the
     // compiler sinks these loads into the block loop, where their counter
@@ -1834,10 +1881,10 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
     T* stage = smem + st.wave * stage_elems<D>();
     store_rows_staged<T, D>(stage, st.dkacc, scale,
                             dk + (int64_t)(start + st.kw0) * sdk.row + (int64_t)hk * sdk.head,
-                            sdk.row, nrows, st.lr, st.g, lane);
+                            sdk.row, nrows, dcols, st.lr, st.g, lane);
     store_rows_staged<T, D>(stage, st.dvacc, 1.0f,
                             dv + (int64_t)(start + st.kw0) * sdv.row + (int64_t)hk * sdv.head,
-                            sdv.row, nrows, st.lr, st.g, lane);
+                            sdv.row, nrows, dcols, st.lr, st.g, lane);
   }
 }
 
@@ -1861,6 +1908,14 @@ int check_tensor(const char* fn, const char* name, const void* p, const int64_t*
   return SCREE_OK;
 }
 
+// head_dim the kernels are instantiated for: every power of two from 16 to
+// 256, with 16 run by the 32-column kernels on zero-padded rows (the dcols
+// argument: loads past it read zeros, stores past it are skipped).
+inline bool head_dim_supported(int head_dim) {
+  return head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
+}
+inline int compute_dim(int head_dim) { return head_dim < 32 ? 32 : head_dim; }
+
 int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, int heads,
                  int head_dim, int dtype, const void* workspace, size_t workspace_bytes) {
   if (!cu) return set_error(SCREE_ERR_INVALID, "%s: cu_seqlens is null", fn);
@@ -1869,9 +1924,9 @@ int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, in
     return set_error(SCREE_ERR_INVALID, "%s: total_tokens %lld out of range", fn, (long long)total);
   if (heads < 1 || heads > 4096)
     return set_error(SCREE_ERR_INVALID, "%s: heads must be in [1, 4096], got %d", fn, heads);
-  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
-    return set_error(SCREE_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (32, 64, 128)", fn,
-                     head_dim);
+  if (!head_dim_supported(head_dim))
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (16, 32, 64, 128, 256)",
+                     fn, head_dim);
   if (dtype != SCREE_DTYPE_F16 && dtype != SCREE_DTYPE_BF16)
     return set_error(SCREE_ERR_UNSUPPORTED, "%s: dtype code %d unsupported (fp16 / bf16 only)", fn,
                      dtype);
@@ -1906,7 +1961,7 @@ inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 // every (item, K/V head, part).
 inline size_t dkv_split_bytes(int64_t tmax, int kv_heads, int gsplit, int head_dim) {
   if (gsplit < 2) return 0;
-  return (size_t)tmax * kv_heads * gsplit * 2 * kBM * head_dim * sizeof(float);
+  return (size_t)tmax * kv_heads * gsplit * 2 * kBM * compute_dim(head_dim) * sizeof(float);
 }
 
 // Head-major block order pays off once every XCD has many rounds of items
@@ -1929,12 +1984,14 @@ inline const int4* schedule_list(const void* ws, int tmax, int head_major) {
 // ~0.6 us at head_dim <= 64 (four or three workgroups per CU) and ~1.2 us at
 // 128 (two): config 4's 1,776 workgroups pay +1.0 us against the scheduler's
 // 3.4, config 5's 22,048 at head_dim 128 +55 us.
-constexpr int64_t kFwdDeriveMaxBlocks = 2048;  // 1024 at head_dim 128
+constexpr int64_t kFwdDeriveMaxBlocks = 2048;  // 1024 at head_dim 128, 512 at 256
 static_assert(kFwdDeriveMaxBlocks < (int64_t)kXcds * 512,
               "a deriving forward's problem must have no head-major pass (attn_head_major)");
 inline bool attn_fwd_derives(int batch, int64_t tmax, int heads, int head_dim) {
   return batch <= kWaveSched &&
-         tmax * heads <= (head_dim <= 64 ? kFwdDeriveMaxBlocks : kFwdDeriveMaxBlocks / 2);
+         tmax * heads <= (head_dim <= 64    ? kFwdDeriveMaxBlocks
+                          : head_dim <= 128 ? kFwdDeriveMaxBlocks / 2
+                                            : kFwdDeriveMaxBlocks / 4);
 }
 inline ItemSource fwd_item_source(void* ws, const int32_t* cu, int batch, int total, int tmax,
                                   int heads, int head_dim, int head_major) {
@@ -1951,7 +2008,7 @@ inline ItemSource list_item_source(const void* ws, int total, int tmax, int head
 template <typename T, int D, bool C>
 void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse,
                   const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
-                  float scale, int tmax, void* ws, int total, hipStream_t stream) {
+                  float scale, int tmax, void* ws, int total, int dcols, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int hm = attn_head_major(heads, tmax);
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
@@ -1959,15 +2016,16 @@ void launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* l
                      static_cast<T*>(o), lse, fwd_item_source(ws, cu, batch, total, tmax, heads, D, hm),
                      tmax, hm,
                      heads, heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
-                     Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e, total);
+                     Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, scale * kLog2e, total,
+                     dcols);
 }
 
 // strides: {dout, q, k, v, o, dq} x {row, head}
 template <typename T, int D, bool C>
 void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void* v, const void* o,
-                     const float* lse, void* dq, float* delta, const int32_t* cu, int batch,
-                     int heads, int kv_heads, const int64_t* st, float scale, int tmax,
-                     const void* ws, int total, hipStream_t stream) {
+                     const float* lse, void* dq, float* delta, const int32_t* /*cu*/,
+                     int /*batch*/, int heads, int kv_heads, const int64_t* st, float scale,
+                     int tmax, const void* ws, int total, int dcols, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads;
   const int hm = attn_head_major(heads, tmax);
   hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, C>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
@@ -1978,15 +2036,17 @@ void launch_bwd_dq_t(const void* dout, const void* q, const void* k, const void*
                      heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
-                     scale * kLog2e, total);
+                     scale * kLog2e, total, dcols);
 }
 
 // strides: {dout, q, k, v, dk, dv} x {row, head}
 template <typename T, int D, bool C>
 void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void* v,
-                      const float* lse, const float* delta, void* dk, void* dv, const int32_t* cu,
-                      int batch, int heads, int kv_heads, const int64_t* st, float scale, int tmax,
-                      const void* ws, int gsplit, float* partial, int total, hipStream_t stream) {
+                      const float* lse, const float* delta, void* dk, void* dv,
+                      const int32_t* /*cu*/, int /*batch*/, int heads, int kv_heads,
+                      const int64_t* st, float scale, int tmax,
+                      const void* ws, int gsplit, float* partial, int total, int dcols,
+                      hipStream_t stream) {
   // one workgroup per (item, K/V head, part of the head group)
   const int64_t grid = (int64_t)tmax * kv_heads * gsplit;
   const int hm = attn_head_major(kv_heads * gsplit, tmax);
@@ -2004,25 +2064,30 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
                      heads / kv_heads,
                      Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
                      Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
-                     scale * kLog2e, gsplit, partial, total);
+                     scale * kLog2e, gsplit, partial, total, dcols);
   if (gsplit > 1)
     hipLaunchKernelGGL((dkv_reduce_kernel<T, D>),
                        dim3((unsigned)((int64_t)tmax * kv_heads * (kBM / kRedRows))), dim3(256), 0,
                        stream, partial, src, tmax, C ? 1 : 0, kv_heads, gsplit, static_cast<T*>(dk),
-                       static_cast<T*>(dv), Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale);
+                       static_cast<T*>(dv), Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
+                       dcols);
 }
 
+// FN<T, compute_dim(head_dim), causal>(...): head_dim 16 runs the 32-column kernels.
+#define SCREE_DISPATCH_T(FN, T, D, causal, ...)                                                  \
+  do {                                                                                           \
+    const int cd_ = compute_dim(D);                                                              \
+    if (cd_ == 32) { if (causal) FN<T, 32, true>(__VA_ARGS__); else FN<T, 32, false>(__VA_ARGS__); } \
+    else if (cd_ == 64) { if (causal) FN<T, 64, true>(__VA_ARGS__); else FN<T, 64, false>(__VA_ARGS__); } \
+    else if (cd_ == 128) { if (causal) FN<T, 128, true>(__VA_ARGS__); else FN<T, 128, false>(__VA_ARGS__); } \
+    else { if (causal) FN<T, 256, true>(__VA_ARGS__); else FN<T, 256, false>(__VA_ARGS__); }   \
+  } while (0)
 #define SCREE_DISPATCH(FN, dtype, D, causal, ...)                                 \
   do {                                                                            \
-    if (dtype == SCREE_DTYPE_F16) {                                               \
-      if (D == 32) { if (causal) FN<f16, 32, true>(__VA_ARGS__); else FN<f16, 32, false>(__VA_ARGS__); } \
-      else if (D == 64) { if (causal) FN<f16, 64, true>(__VA_ARGS__); else FN<f16, 64, false>(__VA_ARGS__); } \
-      else { if (causal) FN<f16, 128, true>(__VA_ARGS__); else FN<f16, 128, false>(__VA_ARGS__); } \
-    } else {                                                                      \
-      if (D == 32) { if (causal) FN<bf16, 32, true>(__VA_ARGS__); else FN<bf16, 32, false>(__VA_ARGS__); } \
-      else if (D == 64) { if (causal) FN<bf16, 64, true>(__VA_ARGS__); else FN<bf16, 64, false>(__VA_ARGS__); } \
-      else { if (causal) FN<bf16, 128, true>(__VA_ARGS__); else FN<bf16, 128, false>(__VA_ARGS__); } \
-    }                                                                             \
+    if (dtype == SCREE_DTYPE_F16)                                                 \
+      SCREE_DISPATCH_T(FN, f16, D, causal, __VA_ARGS__);                          \
+    else                                                                          \
+      SCREE_DISPATCH_T(FN, bf16, D, causal, __VA_ARGS__);                         \
   } while (0)
 
 }  // namespace
@@ -2051,9 +2116,9 @@ extern "C" int scree_attn_schedule(const int32_t* cu_seqlens, int batch, int64_t
   if (total_tokens < 0 || total_tokens > ((int64_t)1 << 30))
     return set_error(SCREE_ERR_INVALID, "%s: total_tokens %lld out of range", fn,
                      (long long)total_tokens);
-  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
-    return set_error(SCREE_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (32, 64, 128)", fn,
-                     head_dim);
+  if (!head_dim_supported(head_dim))
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (16, 32, 64, 128, 256)",
+                     fn, head_dim);
   const size_t need = scree_attn_workspace_bytes(batch, total_tokens, head_dim);
   if (!workspace || workspace_bytes < need)
     return set_error(SCREE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
@@ -2125,7 +2190,7 @@ static int launch_fwd(const char* fn, const void* q, const void* k, const void* 
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, batch, heads,
-                 kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens,
+                 kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens, head_dim,
                  static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
@@ -2244,7 +2309,7 @@ extern "C" int scree_attn_bwd_dq_gqa(const void* dout, const void* q, const void
   const int tmax = (int)tmax_for(batch, total_tokens);
   SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
                  cu_seqlens, batch, heads, kv_heads, strides, softmax_scale, tmax, workspace,
-                 (int)total_tokens, static_cast<hipStream_t>(stream));
+                 (int)total_tokens, head_dim, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
@@ -2291,7 +2356,7 @@ extern "C" int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const voi
                               : nullptr;
   SCREE_DISPATCH(launch_bwd_dkv_t, dtype, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
                  cu_seqlens, batch, heads, kv_heads, strides, softmax_scale, tmax, workspace, gsplit,
-                 partial, (int)total_tokens, static_cast<hipStream_t>(stream));
+                 partial, (int)total_tokens, head_dim, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
@@ -2299,7 +2364,7 @@ extern "C" size_t scree_attn_bwd_workspace_bytes_gqa(int batch, int64_t total_to
                                                      int kv_heads, int head_dim) {
   const size_t base = scree_attn_workspace_bytes(batch, total_tokens, head_dim);
   if (!base || kv_heads < 1 || heads < kv_heads || heads % kv_heads ||
-      (head_dim != 32 && head_dim != 64 && head_dim != 128))
+      !head_dim_supported(head_dim))
     return base;
   const int64_t tmax = tmax_for(batch, total_tokens);
   const int gsplit = dkv_gsplit(tmax, kv_heads, heads / kv_heads);

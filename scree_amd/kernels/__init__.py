@@ -6,7 +6,9 @@ Same signatures as the reference's ``scree.kernels.reference`` functions
 taking and returning
 :class:`scree_amd.Array`.  They run only on ROCm device tensors -- there is no
 CPU implementation here; a host array raises ``TypeError``.  Outputs reuse
-the input's offsets, as the reference does.
+the input's offsets, as the reference does, and are built without
+re-validating them, so none of these calls reads device memory on the host
+(no host synchronisation; tested under ``torch.cuda.set_sync_debug_mode``).
 """
 
 from __future__ import annotations
@@ -26,23 +28,38 @@ def varlen_attention(q: Array, k: Array, v: Array, causal: bool = False) -> Arra
     ``k`` / ``v`` may carry fewer heads than ``q`` (grouped-query attention:
     a divisor of the query heads, each K/V head serving consecutive query
     heads); the reference requires equal head counts.
+
+    Offsets must be identical for q, k, v (``ValueError`` otherwise, as the
+    reference, ``reference/varlen_attention.py:118-119``).  When all three
+    Arrays share one offsets tensor the check is an identity test; distinct
+    tensors are compared on the device, which reads the result on the host.
+    Offsets that decrease somewhere (overlapping sequences; ``Array`` checks
+    only the two ends) make every output and gradient NaN: the device
+    scheduler checks them, so no host read of the offsets is needed.
+
+    Values must be fp16 or bf16, the types the kernels' matrix instructions
+    take, as for the reference's Triton launcher
+    (``triton/varlen_attention.py:215``).  The reference's Array-level torch
+    branch also runs fp32 (``reference/varlen_attention.py:90-113``); here
+    fp32 (or any other dtype) raises ``TypeError`` rather than being computed
+    at a lower precision than the caller asked for.
     """
     import torch
 
     from .hip import varlen_attention_hip_autograd
 
     _require_device(q.values, "varlen_attention")
+    for name, a in (("q", q), ("k", k), ("v", v)):
+        if a.values.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"varlen_attention: {name} is {a.values.dtype}; the HIP kernels take "
+                            "float16 or bfloat16 (cast with .half() or .bfloat16())")
     if not (q.offsets is k.offsets and q.offsets is v.offsets):
         if not (torch.equal(q.offsets, k.offsets) and torch.equal(q.offsets, v.offsets)):
             raise ValueError("q, k, v must have identical offsets")
     if q.ragged_dim != 0:
         raise NotImplementedError("varlen_attention supports ragged_dim=0 only")
-    # Array checks only the two ends; overlapping sequences would give the
-    # scheduler more work than its bound (the kernels then write NaN)
-    if bool((q.offsets[1:] < q.offsets[:-1]).any()):
-        raise ValueError("offsets must be non-decreasing")
     out = varlen_attention_hip_autograd(q.values, k.values, v.values, q.offsets, causal)
-    return Array(values=out, offsets=q.offsets, ragged_dim=0)
+    return Array._trusted(out, q.offsets, 0)
 
 
 def varlen_rmsnorm(arr: Array, weight=None, eps: float = 1e-6) -> Array:
@@ -50,8 +67,7 @@ def varlen_rmsnorm(arr: Array, weight=None, eps: float = 1e-6) -> Array:
     from .hip import varlen_rmsnorm_hip
 
     _require_device(arr.values, "varlen_rmsnorm")
-    return Array(values=varlen_rmsnorm_hip(arr.values, weight, eps), offsets=arr.offsets,
-                 ragged_dim=arr.ragged_dim)
+    return Array._trusted(varlen_rmsnorm_hip(arr.values, weight, eps), arr.offsets, arr.ragged_dim)
 
 
 def varlen_layernorm(arr: Array, weight=None, bias=None, eps: float = 1e-5) -> Array:
@@ -59,8 +75,8 @@ def varlen_layernorm(arr: Array, weight=None, bias=None, eps: float = 1e-5) -> A
     from .hip import varlen_layernorm_hip
 
     _require_device(arr.values, "varlen_layernorm")
-    return Array(values=varlen_layernorm_hip(arr.values, weight, bias, eps), offsets=arr.offsets,
-                 ragged_dim=arr.ragged_dim)
+    return Array._trusted(varlen_layernorm_hip(arr.values, weight, bias, eps), arr.offsets,
+                          arr.ragged_dim)
 
 
 def varlen_add_rmsnorm(arr: Array, residual, weight=None, eps: float = 1e-6):
@@ -81,8 +97,8 @@ def varlen_add_rmsnorm(arr: Array, residual, weight=None, eps: float = 1e-6):
             raise ValueError("arr and residual must have identical offsets")
         residual = residual.values
     h, y = varlen_add_rmsnorm_hip(arr.values, residual, weight, eps)
-    return (Array(values=h, offsets=arr.offsets, ragged_dim=arr.ragged_dim),
-            Array(values=y, offsets=arr.offsets, ragged_dim=arr.ragged_dim))
+    return (Array._trusted(h, arr.offsets, arr.ragged_dim),
+            Array._trusted(y, arr.offsets, arr.ragged_dim))
 
 
 def varlen_softmax(arr: Array) -> Array:
@@ -92,7 +108,7 @@ def varlen_softmax(arr: Array) -> Array:
     if arr.ragged_dim != 0:
         raise NotImplementedError("varlen_softmax supports ragged_dim=0 only in v0.1")
     _require_device(arr.values, "varlen_softmax")
-    return Array(values=varlen_softmax_hip(arr.values, arr.offsets), offsets=arr.offsets, ragged_dim=0)
+    return Array._trusted(varlen_softmax_hip(arr.values, arr.offsets), arr.offsets, 0)
 
 
 __all__ = ["varlen_add_rmsnorm", "varlen_attention", "varlen_layernorm", "varlen_rmsnorm",

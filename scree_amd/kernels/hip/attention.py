@@ -15,8 +15,9 @@ Differences a caller can observe:
 * No host synchronisation: the reference reads ``max(seq_lens)`` with
   ``.item()`` (``varlen_attention.py:220-221``); here a device scheduler turns
   ``cu_seqlens`` into a work list (:func:`attention_schedule`).
-* head_dim must be 32, 64 or 128; q/k/v may be strided views whose last axis
-  is contiguous (other layouts are copied to contiguous first).
+* head_dim must be 16, 32, 64, 128 or 256 (the reference takes any power of
+  two, ``varlen_attention.py:217``); q/k/v may be strided views whose last
+  axis is contiguous (other layouts are copied to contiguous first).
 * Grouped-query attention: ``k`` / ``v`` may have fewer heads than ``q`` (a
   divisor of its head count); query head ``h`` attends with K/V head
   ``h // (q_heads // kv_heads)`` and ``dk`` / ``dv`` sum over each group.

@@ -4,8 +4,9 @@ Device counterparts of ``scree.to_padded`` / ``scree.from_padded``
 (``src/scree/_core.py:161-301``), whose torch branch copies one slice per
 sequence in a host loop and reads each mask row's length with ``.item()``.
 Here ``to_padded_hip`` is one launch (after a single host read of the
-offsets to size the output) and ``from_padded_hip`` is a count/scan launch,
-one host read of the total, and one gather launch.  Semantics follow the
+offsets to size the output, skipped when the caller passes ``max_len``) and
+``from_padded_hip`` is a count/scan launch, one host read of the total
+(skipped when the caller passes ``total``), and one gather launch.  Semantics follow the
 reference exactly: ``mask`` True on valid rows; left or right padding;
 ``from_padded`` takes the first ``mask[i].sum()`` rows of each batch row
 (right padding assumed, ``_core.py:269-285``).
@@ -62,8 +63,17 @@ def to_padded_hip(values, offsets, side="right", fill_value=0.0, max_len=None):
     return padded, mask
 
 
-def from_padded_hip(padded, mask):
-    """``(values, offsets)`` from right-padded ``padded`` (B, T, *features) and ``mask`` (B, T)."""
+def from_padded_hip(padded, mask, total=None):
+    """``(values, offsets)`` from right-padded ``padded`` (B, T, *features) and ``mask`` (B, T).
+
+    The number of rows of ``values`` is ``mask.sum()``, a device value: it
+    is read on the host (one synchronisation, as ``torch.masked_select``
+    makes) unless the caller passes it as ``total``.  A ``total`` below the
+    true count keeps the first ``total`` rows (the gather clamps every
+    sequence to the output, so nothing is written past it), and then
+    ``offsets[-1]`` disagrees with ``values.shape[0]``, which
+    :class:`scree_amd.Array` rejects.
+    """
     assert padded.is_cuda, "from_padded on HIP requires ROCm device tensors"
     batch, t = int(padded.shape[0]), int(padded.shape[1])
     if batch < 1:
@@ -75,7 +85,11 @@ def from_padded_hip(padded, mask):
     with _ffi.device_guard(pad.device):
         _ffi.check(_ffi.lib().scree_padded_offsets(
             _ffi.ptr(m), batch, t, _ffi.ptr(offsets), _ffi.stream_of(pad)))
-        total = int(offsets[-1].item())
+        if total is None:
+            total = int(offsets[-1].item())
+        total = int(total)
+        if total < 0:
+            raise ValueError(f"total must be non-negative, got {total}")
         values = torch.empty((total, *pad.shape[2:]), dtype=pad.dtype, device=pad.device)
         _ffi.check(_ffi.lib().scree_from_padded(
             _ffi.ptr(pad), _ffi.ptr(offsets), batch, t, _row_bytes(pad, 2), total,

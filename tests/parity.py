@@ -66,12 +66,20 @@ def check_close(name, got, want, atol, extra=None, unit=0.0):
     return max_abs
 
 
-def reference_excess(q, k, v, do, off, causal, dtype):
+def reference_excess(q, k, v, do, off, causal, dtype, o=None, lse=None):
     """``E_ref`` per output (O, dQ, dK, dV): max(|emulated - exact| - u|exact|, 0)
     for the reference kernels' arithmetic in ``dtype`` on these fp64 inputs.
 
-    The exact backward is evaluated at the emulated O (the gradients depend on
-    O through Delta), as the tests evaluate it at the HIP O.
+    The backward's inputs include the forward's O and LSE.  Given ``o`` and
+    ``lse`` (the ones the HIP backward consumed), the reference backward is
+    emulated on exactly those, and the exact backward is evaluated at that O
+    (the gradients depend on O through Delta), as the tests evaluate it.
+    Without them both use the emulated reference forward's O and LSE.  The
+    distinction matters at large logits in bf16: a different O moves every
+    Delta, which re-draws the rounding of dS, and the largest excess of dK
+    then moves by up to 40% (12.7e-3 -> 17.8e-3 on one D = 16 case, for the
+    reference's own arithmetic) -- more than the flat bound that separates the
+    two sides of the comparison.
     """
     from oracle.attention import (attention_bwd, attention_bwd_rounded, attention_fwd,
                                   attention_fwd_rounded)
@@ -83,8 +91,10 @@ def reference_excess(q, k, v, do, off, causal, dtype):
     ex = lambda got, ref: max(0.0, float((np.abs(got - ref) - u * np.abs(ref)).max()))  # noqa: E731
     out = {"O": ex(eo, ro)}
     if do is not None:
-        emul = attention_bwd_rounded(do, q, k, v, eo, el, off, causal=causal, operand=operand)
-        exact = attention_bwd(do, q, k, v, eo, rl, off, causal=causal)
+        bo = eo if o is None else o
+        bl = el if lse is None else lse
+        emul = attention_bwd_rounded(do, q, k, v, bo, bl, off, causal=causal, operand=operand)
+        exact = attention_bwd(do, q, k, v, bo, rl, off, causal=causal)
         for name, a, b in zip(("dQ", "dK", "dV"), emul, exact):
             out[name] = ex(a, b)
     return out

@@ -46,9 +46,11 @@ def test_attention_validation_errors():
     # null cu_seqlens
     rc = lib.scree_attn_fwd(p, p, p, p, p, null, 2, 10, 16, 64, strides, 0.125, 1, 1, p, 1 << 16, null)
     assert rc == _ffi.SCREE_ERR_INVALID and "cu_seqlens" in _err()
-    # unsupported head_dim
-    rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 48, strides, 0.125, 1, 1, p, 1 << 16, null)
-    assert rc == _ffi.SCREE_ERR_UNSUPPORTED and "head_dim" in _err()
+    # unsupported head_dim: powers of two from 16 to 256 only
+    for bad_dim in (8, 48, 512):
+        rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, bad_dim, strides, 0.125, 1, 1, p,
+                                1 << 16, null)
+        assert rc == _ffi.SCREE_ERR_UNSUPPORTED and "head_dim" in _err()
     # fp32 is not an attention dtype
     rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 64, strides, 0.125, 1, 0, p, 1 << 16, null)
     assert rc == _ffi.SCREE_ERR_UNSUPPORTED and "dtype" in _err()
@@ -82,6 +84,9 @@ def test_workspace_sizes():
     assert lib.scree_attn_needs_schedule(16, 12160, 19, 64) == 1    # 2109
     assert lib.scree_attn_needs_schedule(16, 12160, 9, 128) == 0    # 999
     assert lib.scree_attn_needs_schedule(16, 12160, 10, 128) == 1   # 1110
+    assert lib.scree_attn_needs_schedule(16, 12160, 4, 256) == 0    # 444: 512 at head_dim 256
+    assert lib.scree_attn_needs_schedule(16, 12160, 5, 256) == 1    # 555
+    assert lib.scree_attn_needs_schedule(16, 12160, 18, 16) == 0    # head_dim 16 runs as 32
     assert lib.scree_attn_needs_schedule(64, 1024, 1, 64) == 0
     assert lib.scree_attn_needs_schedule(65, 1024, 1, 64) == 1      # past one wavefront of sequences
     assert lib.scree_attn_needs_schedule(0, 10, 4, 64) == 1         # invalid: the call will say why

@@ -43,7 +43,8 @@ def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True, kv_head
             return check_attn(name, got, want, atol, dtype, e_ref[name])
         return check_close(name, got, want, atol)
 
-    e_ref = reference_excess(q64, k64, v64, do64, off, causal, dtype) if bf16 else None
+    e_ref = (reference_excess(q64, k64, v64, do64, off, causal, dtype, o=np64(out),
+                              lse=lse.cpu().numpy().astype(np.float64)) if bf16 else None)
     check("O", np64(out), ref_o, 2e-3)
     check_close("LSE", lse.cpu().numpy().astype(np.float64), ref_lse, 1e-4 + 1e-5 * np.abs(ref_lse).max())
     if not backward:
@@ -56,14 +57,14 @@ def _run_case(lengths, heads, dim, dtype, causal, seed=0, backward=True, kv_head
     check("dV", np64(dv), rdv, 5e-3)
 
 
-@pytest.mark.parametrize("dim", [32, 64, 128])
+@pytest.mark.parametrize("dim", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("causal", [True, False])
 def test_edge_lengths(dim, dtype, causal):
     _run_case(EDGE_LENGTHS, 2, dim, dtype, causal, seed=dim)
 
 
-@pytest.mark.parametrize("dim", [32, 64, 128])
+@pytest.mark.parametrize("dim", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("causal", [True, False])
 def test_grouped_query_edge_lengths(dim, dtype, causal):
@@ -317,7 +318,8 @@ def test_config5_sampled_heads_bf16():
         q64, k64, v64, do64 = sub(q), sub(k), sub(v), sub(do)
         loff = np.array([0, b - a], dtype=np.int32)
         ro, rl = attention_fwd(q64, k64, v64, loff, causal=True, dtype=np.float64)
-        e_ref = reference_excess(q64, k64, v64, do64, loff, True, torch.bfloat16)
+        e_ref = reference_excess(q64, k64, v64, do64, loff, True, torch.bfloat16, o=sub(out),
+                                 lse=lse[a:b][:, heads].cpu().numpy().astype(np.float64))
         check_attn("O", sub(out), ro, 2e-3, torch.bfloat16, e_ref["O"])
         check_close("LSE", lse[a:b][:, heads].cpu().numpy().astype(np.float64), rl, 1e-4 + 1e-5 * np.abs(rl).max())
         rdq, rdk, rdv, _ = attention_bwd(do64, q64, k64, v64, sub(out), rl, loff, causal=True)

@@ -34,6 +34,21 @@ def test_config1_attention_fwd_bwd(dtype, causal):
     _run_case(lengths, 4, 32, dtype, causal, seed=1, backward=True)
 
 
+def test_config1_fp32_attention_raises_type_error():
+    """Config 1 is stated in fp32.  The Array-level call takes only the half
+    types the kernels compute in and says so, instead of computing fp32
+    inputs at a lower precision."""
+    import scree_amd
+    from scree_amd.kernels import varlen_attention
+
+    say("case: config1 fp32 Array-level attention -> TypeError")
+    lengths = workloads.config1_lengths()
+    _, cu = cu_of(lengths)
+    x = scree_amd.Array(values=randn((sum(lengths), 4, 32), torch.float32, 2), offsets=cu)
+    with pytest.raises(TypeError, match="float16 or bfloat16"):
+        varlen_attention(x, x, x, causal=True)
+
+
 @pytest.mark.parametrize("shape", [(1980, 4, 32), (1980, 128)])
 def test_config1_rmsnorm_fp32_unit_gamma(shape):
     from scree_amd.kernels.hip import varlen_rmsnorm_hip

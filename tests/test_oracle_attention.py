@@ -381,3 +381,24 @@ def test_rounded_variant_matches_torch_casts(operand, dt, causal):
     assert err.max() > 0.1 * u
     assert (err <= u * (np.abs(v).max() + np.abs(exact_o)) + 1e-12).all()
     np.testing.assert_allclose(lse, exact_lse, atol=1e-12)  # the row sum is unrounded
+
+
+def test_reference_excess_emulates_the_backward_on_the_given_forward_outputs():
+    """``reference_excess`` runs the reference backward's arithmetic on the O and
+    LSE it is given (the HIP forward's, in the GPU tests): given the emulated
+    reference forward's own outputs it reproduces the default, and given
+    another O its backward figures change while the forward's do not."""
+    from oracle.attention import attention_fwd_rounded
+    from parity import reference_excess
+
+    q, k, v, off = _inputs([150, 1, 64, 65], 2, 32, seed=11)
+    q, k = 2.0 * q, 2.0 * k
+    do = np.random.default_rng(12).standard_normal(q.shape)
+    eo, el = attention_fwd_rounded(q, k, v, off, causal=True, operand="bfloat16")
+    base = reference_excess(q, k, v, do, off, True, torch.bfloat16)
+    same = reference_excess(q, k, v, do, off, True, torch.bfloat16, o=eo, lse=el)
+    assert base == same
+    other_o = torch.from_numpy(eo + 2.0 ** -7 * np.abs(eo)).bfloat16().double().numpy()
+    other = reference_excess(q, k, v, do, off, True, torch.bfloat16, o=other_o, lse=el)
+    assert other["O"] == base["O"]
+    assert any(other[g] != base[g] for g in ("dQ", "dK", "dV"))

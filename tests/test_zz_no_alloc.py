@@ -1,8 +1,12 @@
 """The allocation-free attention forward (scree_attn_fwd_noalloc) against the
 workspace forward it is a variant of (scheduler + scree_attn_fwd_gqa on a
-caller-owned workspace): bit-identical outputs and LSE, on two calls in a row
-whose second is smaller than the first (so a stale schedule left in the
-static array would show), plus the host-side size limit."""
+caller-owned workspace): bit-identical outputs and LSE, on calls in a row of
+decreasing size, plus the host-side size limit.  The sequence of calls
+alternates the two ways the entry point gets its items: a forward that
+derives them from the offsets (scree_attn_needs_schedule == 0) never reads
+the static array, so the calls that schedule (100 sequences, past the
+derivation's 64) sit between deriving calls of other sizes, where a stale or
+misaddressed schedule in the static array would change the output."""
 
 import ctypes
 import math
@@ -78,11 +82,20 @@ def test_limit_is_rejected_before_any_launch():
 def test_two_calls_match_the_workspace_forward():
     big = workloads.config3().lengths        # 12160 tokens, 16 x 64, fp16, causal
     small = [300, 17, 129, 640, 1]           # smaller: a stale schedule would cover more work
-    cases = [(big, 16, 16, 64, torch.float16, True), (small, 8, 2, 128, torch.bfloat16, False)]
+    rng = np.random.default_rng(5)
+    many = [int(x) for x in rng.integers(1, 200, size=100)]   # > 64 sequences: scheduled
+    fewer = [int(x) for x in rng.integers(1, 120, size=70)]   # scheduled, smaller than `many`
+    cases = [(big, 16, 16, 64, torch.float16, True),          # derives
+             (many, 4, 4, 64, torch.float16, True),           # schedules into the static array
+             (small, 8, 2, 128, torch.bfloat16, False),       # derives
+             (fewer, 4, 2, 64, torch.bfloat16, False)]        # schedules again, smaller
+    lib = _ffi.lib()
     first = None
     for i, (lengths, h, hk, d, dt, causal) in enumerate(cases):
+        scheduled = bool(lib.scree_attn_needs_schedule(len(lengths), sum(lengths), h, d))
+        assert scheduled == (len(lengths) > 64)
         say(f"case: noalloc call {i}: B={len(lengths)} N={sum(lengths)} H={h} Hkv={hk} D={d} "
-            f"{dt} causal={causal}")
+            f"{dt} causal={causal} scheduled={scheduled}")
         cu, q, k, v = _inputs(lengths, h, hk, d, dt, 80 + i)
         got_o, got_l = _noalloc(cu, q, k, v, causal)
         torch.cuda.synchronize()
