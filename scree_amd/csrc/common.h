@@ -112,6 +112,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Sum of v over the wave, complete in lane 63 only (other lanes hold partial
+// sums): DPP row shifts add each row of 16 lanes into its last lane, then
+// row broadcasts carry rows 0 and 2 into rows 1 and 3 and row 1 into rows 2
+// and 3 -- VALU operations only, where wave_sum's shuffles go through LDS.
+__device__ __forceinline__ float wave_sum_last(float v) {
+  // dpp_ctrl: row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xf, 0xf, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xf, 0xf, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xf, 0xf, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
+  return v;
+}
+
 // --------------------------------------------------------------------- MFMA
 // C(32x32, f32) += A(32x16) * B(16x32); lane l holds A row l%32 / B column
 // l%32 with k = 8*(l/32) .. +7; C element i of lane l is row

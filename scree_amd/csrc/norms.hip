@@ -267,41 +267,46 @@ struct BwdRows {
 
 // The rows of one step: row sums reduced across the wave by shuffles and
 // across the block through red[buf] (one barrier), then dx written and the
-// parameter gradients accumulated in aw / ab.
+// parameter gradients accumulated in aw / ab.  `wf` holds this thread's
+// weights as fp32 (ones without a weight).  Per row, x-hat = x * rstd - mean
+// * rstd is one FMA and the output folds its row constants into two more:
+//   LayerNorm  dx = rstd * g - rstd*b * x-hat - rstd*a,  a = mean(g), b = mean(g * x-hat)
+//   RMSNorm    dx = rstd * g - k * x,                    k = rstd^3 * mean(g * x)
+// with g = dy * w (reference varlen_layernorm.py:64-74, varlen_rmsnorm.py:58-65).
 template <typename T, int CPT, int R, bool LAYER, bool RES>
 __device__ __forceinline__ void norm_bwd_step(BwdRows<T, CPT, R, LAYER, RES>& st,
                                               float (&red)[2][R][2][kBwdWarps], int buf,
-                                              const uint4* wv, const bool* own, bool has_w,
+                                              const float (&wf)[CPT][16 / sizeof(T)],
+                                              const bool* own,
                                               float (&aw)[CPT][16 / sizeof(T)],
                                               float (&ab)[LAYER ? CPT : 1][16 / sizeof(T)],
                                               T* __restrict__ dx, int64_t rb, int64_t r1, int dim,
-                                              int tid) {
+                                              float inv_dim, int tid) {
   constexpr int VEC = 16 / sizeof(T);
   const int lane = tid & (kWave - 1), wave = tid / kWave;
-  const float fdim = (float)dim;
-  float s1[R], s2[R];
+  float s1[R], s2[R], nmr[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     s1[r] = 0.f;
     s2[r] = 0.f;
+    nmr[r] = -st.mu[r] * st.rs[r];
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float xx = elem<T>(st.xv[r][k], e);
-        const float d = elem<T>(st.gv[r][k], e);
-        const float g = has_w ? d * elem<T>(wv[k], e) : d;
+        const float g = elem<T>(st.gv[r][k], e) * wf[k][e];
         if (LAYER) {
           s1[r] += g;
-          s2[r] += g * ((xx - st.mu[r]) * st.rs[r]);
+          s2[r] = fmaf(g, fmaf(xx, st.rs[r], nmr[r]), s2[r]);
         } else {
-          s1[r] += xx * g;
+          s1[r] = fmaf(xx, g, s1[r]);
         }
       }
-    s1[r] = wave_sum(s1[r]);
-    if (LAYER) s2[r] = wave_sum(s2[r]);
+    s1[r] = wave_sum_last(s1[r]);
+    if (LAYER) s2[r] = wave_sum_last(s2[r]);
   }
-  if (lane == 0) {
+  if (lane == kWave - 1) {  // the wave's sums are complete in its last lane
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       red[buf][r][0][wave] = s1[r];
@@ -332,8 +337,10 @@ __device__ __forceinline__ void norm_bwd_step(BwdRows<T, CPT, R, LAYER, RES>& st
     const int64_t row = rb + r;
     if (row >= r1) continue;
     const float rr = st.rs[r];
-    const float k_rms = rr * rr * rr * t1 / fdim;
-    const float a_ln = t1 / fdim, b_ln = t2 / fdim;
+    // LayerNorm: c1 = -rstd * mean(g), c2 = -rstd * mean(g * x-hat);
+    // RMSNorm: c2 = -rstd^3 * mean(g * x).
+    const float c1 = -rr * (t1 * inv_dim);
+    const float c2 = LAYER ? -rr * (t2 * inv_dim) : -(rr * rr * rr) * (t1 * inv_dim);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       if (!own[k]) continue;
@@ -342,15 +349,15 @@ __device__ __forceinline__ void norm_bwd_step(BwdRows<T, CPT, R, LAYER, RES>& st
       for (int e = 0; e < VEC; ++e) {
         const float xx = elem<T>(st.xv[r][k], e);
         const float d = elem<T>(st.gv[r][k], e);
-        const float g = has_w ? d * elem<T>(wv[k], e) : d;
+        const float g = d * wf[k][e];
         if (LAYER) {
-          const float xh = (xx - st.mu[r]) * rr;
-          f[e] = rr * (g - a_ln - xh * b_ln);
-          aw[k][e] += d * xh;
+          const float xh = fmaf(xx, rr, nmr[r]);
+          f[e] = fmaf(rr, g, fmaf(c2, xh, c1));
+          aw[k][e] = fmaf(d, xh, aw[k][e]);
           ab[LAYER ? k : 0][e] += d;
         } else {
-          f[e] = rr * g - k_rms * xx;
-          aw[k][e] += d * xx * rr;
+          f[e] = fmaf(rr, g, c2 * xx);
+          aw[k][e] = fmaf(d * rr, xx, aw[k][e]);
         }
         if (RES) f[e] += elem<T>(st.hv[RES ? r : 0][k], e);
       }
@@ -372,13 +379,15 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
   const int tid = threadIdx.x;
   const int nvec = dim / VEC;
 
-  uint4 wv[CPT];
+  float wf[CPT][VEC];  // this thread's weights as fp32, ones without a weight
   bool own[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int v = tid + k * kBwdThreads;
     own[k] = v < nvec;
-    wv[k] = (w && own[k]) ? ld16(w + (int64_t)v * VEC) : make_uint4(0, 0, 0, 0);
+    const uint4 wv = (w && own[k]) ? ld16(w + (int64_t)v * VEC) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) wf[k][e] = w ? elem<T>(wv, e) : 1.0f;
   }
   float aw[CPT][VEC], ab[LAYER ? CPT : 1][VEC];
 #pragma unroll
@@ -393,16 +402,16 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_cols(
   // load.  Steps are S rows apart; rows past the end load as zeros and are
   // not written.
   BwdRows<T, CPT, R, LAYER, RES> A, B;
-  const bool has_w = w != nullptr;
+  const float inv_dim = 1.0f / (float)dim;
   const int64_t S = (int64_t)gridDim.x * R;
   const int64_t first = (int64_t)blockIdx.x * R;
   if (first < rows) A.load(x, dy, dres, mean_in, rstd_in, own, first, rows, dim, tid);
   for (int64_t rb = first; rb < rows; rb += 2 * S) {
     if (rb + S < rows) B.load(x, dy, dres, mean_in, rstd_in, own, rb + S, rows, dim, tid);
-    norm_bwd_step<T, CPT, R, LAYER, RES>(A, red, 0, wv, own, has_w, aw, ab, dx, rb, rows, dim, tid);
+    norm_bwd_step<T, CPT, R, LAYER, RES>(A, red, 0, wf, own, aw, ab, dx, rb, rows, dim, inv_dim, tid);
     if (rb + S >= rows) break;
     if (rb + 2 * S < rows) A.load(x, dy, dres, mean_in, rstd_in, own, rb + 2 * S, rows, dim, tid);
-    norm_bwd_step<T, CPT, R, LAYER, RES>(B, red, 1, wv, own, has_w, aw, ab, dx, rb + S, rows, dim, tid);
+    norm_bwd_step<T, CPT, R, LAYER, RES>(B, red, 1, wf, own, aw, ab, dx, rb + S, rows, dim, inv_dim, tid);
   }
   for (int p = 0; p < nparam; ++p) {
     float* out = partial + ((int64_t)blockIdx.x * nparam + p) * dim;
@@ -530,13 +539,21 @@ __global__ __launch_bounds__(256) void norm_param_colsum4(const float* __restric
   if ((gridDim.x & 7) == 0) slab = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   const int col = slab * 16 + cq * 4;
   const int p = blockIdx.y;
-  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (col < dim) {
-#pragma unroll 4
-    for (int i = rg; i < nparts; i += 64) {
-      const float4 v = *reinterpret_cast<const float4*>(partial + ((int64_t)i * nparam + p) * dim + col);
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
-    }
+  // Every load in flight at once (at most kMaxParts / 64 per thread), then
+  // the sum in row order.
+  constexpr int kIt = kMaxParts / 64;
+  float4 v[kIt];
+#pragma unroll
+  for (int j = 0; j < kIt; ++j) {
+    const int i = rg + 64 * j;
+    v[j] = (col < dim && i < nparts)
+               ? *reinterpret_cast<const float4*>(partial + ((int64_t)i * nparam + p) * dim + col)
+               : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float4 s = v[0];
+#pragma unroll
+  for (int j = 1; j < kIt; ++j) {
+    s.x += v[j].x; s.y += v[j].y; s.z += v[j].z; s.w += v[j].w;
   }
   red[rg][cq] = s;
   __syncthreads();
