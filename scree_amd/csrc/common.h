@@ -106,10 +106,11 @@ __device__ __forceinline__ void st16_nt(void* p, const uint4& v) {
 }
 
 // ------------------------------------------------------------- reductions
+__device__ __forceinline__ float wave_sum_last(float v);
+// Sum of v over the wave, in every lane (the DPP sum read back from lane 63
+// as a wave-uniform value).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_last(v)), 63));
 }
 
 // Sum of v over the wave, complete in lane 63 only (other lanes hold partial
