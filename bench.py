@@ -307,6 +307,9 @@ def time_norms(cfg, steps, warmup):
                           rows * row + pad_rows * (row + 1))
     cases["from_padded_user_call"] = (lambda: Pd.from_padded_hip(padded, pmask),
                                       pad_rows + 2.0 * rows * row)
+    # the same call given the token count (no host read of the device total)
+    cases["from_padded_given_total"] = (lambda: Pd.from_padded_hip(padded, pmask, total=rows),
+                                        pad_rows + 2.0 * rows * row)
     out = {}
     for name, (fn, nbytes) in cases.items():
         for _ in range(warmup):
