@@ -144,3 +144,27 @@ def test_rising_scores_reach_the_rescale_path(dim, dtype, causal):
     v, do = _normal((n, 2, dim), 7), _normal((n, 2, dim), 8)
     q, k, v, do = (t.to(dtype).cuda() for t in (q, k, v, do))
     _check(q, k, v, do, off, cu, causal, dtype, 12.0)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_rising_scores_past_fp32_range(dim, dtype, causal):
+    """The rising-score construction with later keys ~200 nats (~290 log2
+    units) above the first ones: weights formed against the first tile's
+    maximum overflow fp32 (2^128), so the forward's rescale cannot scale
+    them and must form them again from the scores."""
+    lengths = [400, 130]
+    n = sum(lengths)
+    say(f"case: rising scores past fp32 range lengths={lengths} H=2 D={dim} {dtype} causal={causal}")
+    off, cu = cu_of(lengths)
+    g = torch.Generator().manual_seed(91 + dim)
+    u = torch.where(torch.rand(2, dim, generator=g) < 0.5, -1.0, 1.0)
+    pos = torch.cat([torch.arange(L, dtype=torch.float32) / max(L - 1, 1) for L in lengths])
+    beta = 200.0 / math.sqrt(dim)
+    q = _normal((n, 2, dim), 15) + u
+    k = _normal((n, 2, dim), 16) + beta * pos[:, None, None] * u
+    v, do = _normal((n, 2, dim), 17), _normal((n, 2, dim), 18)
+    q, k, v, do = (t.to(dtype).cuda() for t in (q, k, v, do))
+    _check(q, k, v, do, off, cu, causal, dtype, 130.0)
+
