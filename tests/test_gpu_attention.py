@@ -173,6 +173,18 @@ def test_batches_past_one_wavefront(batch, causal):
     _run_case(lengths, 2, 64, torch.float16, causal, seed=batch)
 
 
+@pytest.mark.parametrize("dim,dtype", [(16, torch.float16), (256, torch.bfloat16)])
+def test_scheduled_batches_at_the_extreme_head_dims(dim, dtype):
+    """head_dim 16 (the 32-column kernels on zero-padded rows) and 256 (one
+    wave per SIMD) past 64 sequences, where the forward reads the scheduler's
+    list instead of deriving its items, with grouped K/V heads."""
+    rng = np.random.default_rng(dim)
+    lengths = [int(x) for x in rng.integers(0, 260, size=90)]
+    lengths[7] = 0
+    lengths[-1] = 513
+    _run_case(lengths, 4, dim, dtype, True, seed=dim + 3, kv_heads=2)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_batch_past_the_sorting_scheduler(causal):
     """2,500 sequences (beyond the 2,048 the sorting scheduler holds in LDS):
