@@ -13,8 +13,11 @@
  *     scree_last_error() returns a message for the calling thread's last
  *     failure.
  *   - dtype codes: SCREE_DTYPE_F32 / F16 / BF16.  Attention takes F16 or
- *     BF16 (as the reference's GPU launcher asserts,
- *     src/scree/kernels/triton/varlen_attention.py:213-215); the norms take
+ *     BF16 on the matrix-instruction kernels (the types the reference's GPU
+ *     launcher asserts, src/scree/kernels/triton/varlen_attention.py:213-215)
+ *     and F32 on FP32-FMA kernels (what the reference's Array-level torch
+ *     branch computes fp32 arrays with, reference/varlen_attention.py:90-113:
+ *     every operand stays fp32; no grouped-query dK/dV split); the norms take
  *     all three.
  *   - `cu_seqlens` is the int32 offsets vector of length batch+1 (the
  *     scree.Array `offsets`, src/scree/_core.py:22-62), resident on the

@@ -1888,6 +1888,330 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
   }
 }
 
+// ---------------------------------------------------------- fp32 attention
+// fp32 inputs, which the reference's Array-level function computes as given
+// (its torch branch, reference/varlen_attention.py:90-113).  The matrix
+// instructions run fp32 at a sixteenth of their 16-bit rate, so these kernels
+// use FP32 FMAs instead: each row of an item is split over TPR = D / DPT
+// threads (consecutive lanes of one wave) holding DPT consecutive columns, a
+// dot product is DPT FMAs plus a sum over those lanes, and K / V (or Q / dO)
+// rows are staged 32 at a time in LDS, where every row group reads the same
+// staged row (a broadcast).  A workgroup of at most 512 threads covers its
+// item's 128 rows in 128 / RPP passes of RPP rows (2 at head_dim 128, 4 at
+// 256).  Scores, weights, sums and accumulators are fp32; the forward takes
+// each 32-key tile's maximum before forming its weights, so every weight is
+// at most 1, as in the reference's max-subtracted softmax.  Every sum over
+// keys or queries is taken per 32-row tile first and then over the tiles,
+// which keeps its rounding error near that of the blocked sums of a GEMM
+// (a group of 4 heads over 1,000 queries otherwise added 3x the reference's
+// own fp32 error to dV).  Same work lists, item order and failure handling
+// as the 16-bit kernels.
+template <int D>
+constexpr int f32_dpt() {
+  return 16;
+}
+template <int D>
+constexpr int f32_tpr() {
+  return D / f32_dpt<D>();  // 1 to 16
+}
+template <int D>
+constexpr int f32_rows() {
+  return kBM * f32_tpr<D>() <= 512 ? kBM : 512 / f32_tpr<D>();  // rows per pass
+}
+template <int D>
+constexpr int f32_threads() {
+  return f32_rows<D>() * f32_tpr<D>();
+}
+constexpr int kF32Rows = 32;  // keys (forward, dQ) or queries (dK/dV) per LDS tile
+
+// Sum over the TPR consecutive lanes of one row (TPR divides 64).
+template <int TPR>
+__device__ __forceinline__ float row_sum(float x) {
+#pragma unroll
+  for (int m = 1; m < TPR; m <<= 1) x += __shfl_xor(x, m, kWave);
+  return x;
+}
+template <int N>
+__device__ __forceinline__ void load_slice(float (&dst)[N], const float* p) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p + i);
+    dst[i] = t.x, dst[i + 1] = t.y, dst[i + 2] = t.z, dst[i + 3] = t.w;
+  }
+}
+template <int N>
+__device__ __forceinline__ void store_slice(float* __restrict__ p, const float (&src)[N], float mul) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4)
+    *reinterpret_cast<float4*>(p + i) =
+        make_float4(src[i] * mul, src[i + 1] * mul, src[i + 2] * mul, src[i + 3] * mul);
+}
+template <int N>
+__device__ __forceinline__ float dot_slice(const float (&a)[N], const float (&b)[N]) {
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; i += 2) {
+    s0 = fmaf(a[i], b[i], s0);
+    s1 = fmaf(a[i + 1], b[i + 1], s1);
+  }
+  return s0 + s1;
+}
+template <int N>
+__device__ __forceinline__ void axpy_slice(float (&acc)[N], float a, const float (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc[i] = fmaf(a, x[i], acc[i]);
+}
+// Rows [row0, row0 + kF32Rows) of a head's (tokens, D) rows at `base` into
+// `lds` (row-major, D floats per row); rows >= limit become zeros.
+template <int D>
+__device__ __forceinline__ void stage_rows_f32(float* lds, const float* __restrict__ base,
+                                               int64_t row_stride, int row0, int limit) {
+  constexpr int C4 = D / 4;
+  for (int idx = threadIdx.x; idx < kF32Rows * C4; idx += blockDim.x) {
+    const int r = idx / C4, c = 4 * (idx % C4);
+    const int row = row0 + r;
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < limit) t = *reinterpret_cast<const float4*>(base + (int64_t)row * row_stride + c);
+    *reinterpret_cast<float4*>(lds + r * D + c) = t;
+  }
+}
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(f32_threads<D>()) void attn_fwd_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ o, float* __restrict__ lse, ItemSource src, int tmax, int head_major,
+    int heads, int group, Strides sq, Strides sk, Strides sv, Strides so, float scale, int total) {
+  constexpr int DPT = f32_dpt<D>(), TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
+  __shared__ __align__(16) float sK[KT * D];
+  __shared__ __align__(16) float sV[KT * D];
+  const ItemView iv = item_view<true>(src, tmax);
+  if (iv.failed) {
+    publish_header(src, iv, CAUSAL ? 1 : 0);
+    poison_rows(o, so, total, heads, D);
+    poison_stats(lse, total, heads);
+    return;
+  }
+  int item, h;
+  if (!map_block(heads, tmax, head_major, group, false, item, h) || item >= iv.count) {
+    publish_header(src, iv, CAUSAL ? 1 : 0);
+    return;
+  }
+  const int4 it = item_at<true>(src, iv, CAUSAL, item);
+  if (it.w == 0) return;
+  const int start = it.z, L = it.w, q0 = it.y * kBM;
+  const int hk = h / group;
+  const int c0 = (threadIdx.x % TPR) * DPT;
+  const float* kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
+  const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
+  const int kend = CAUSAL ? min(L, q0 + kBM) : L;
+  for (int r0 = 0; r0 < kBM && q0 + r0 < L; r0 += RPP) {
+    const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
+    // rows past L compute on row L-1 and store nothing
+    float qv[DPT], ov[DPT];
+    load_slice(qv, q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head + c0);
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) ov[i] = 0.f;
+    float m = kNegInf, l = 0.f;
+    const int qlim = CAUSAL ? min(my_q, L - 1) : L - 1;  // the last key this row sees
+    const int kpass = CAUSAL ? min(kend, q0 + r0 + RPP) : kend;
+    for (int kb = 0; kb < kpass; kb += KT) {
+      __syncthreads();  // the previous tile is consumed
+      stage_rows_f32<D>(sK, kh, sk.row, kb, kend);
+      stage_rows_f32<D>(sV, vh, sv.row, kb, kend);
+      __syncthreads();
+      float s[KT];
+      float tile_m = kNegInf;
+#pragma unroll
+      for (int i = 0; i < KT; ++i) {
+        float kr[DPT];
+        load_slice(kr, sK + i * D + c0);
+        const float dotv = row_sum<TPR>(dot_slice(qv, kr)) * scale;
+        s[i] = kb + i <= qlim ? dotv : kNegInf;
+        tile_m = fmaxf(tile_m, s[i]);
+      }
+      // key 0 is in every row's first tile, so m is finite from then on
+      const float m_new = fmaxf(m, tile_m);
+      const float alpha = fast_exp2((m - m_new) * kLog2e);
+      float ot[DPT], lt = 0.f;
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) ot[d] = 0.f;
+#pragma unroll 4
+      for (int i = 0; i < KT; ++i) {
+        const float p = fast_exp2((s[i] - m_new) * kLog2e);
+        float vr[DPT];
+        load_slice(vr, sV + i * D + c0);
+        lt += p;
+        axpy_slice(ot, p, vr);
+      }
+      l = fmaf(l, alpha, lt);
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) ov[d] = fmaf(ov[d], alpha, ot[d]);
+      m = m_new;
+    }
+    if (my_q < L) {
+      store_slice(o + (int64_t)(start + my_q) * so.row + (int64_t)h * so.head + c0, ov, 1.0f / l);
+      if (c0 == 0) lse[(int64_t)(start + my_q) * heads + h] = m + logf(l);
+    }
+  }
+  publish_header(src, iv, CAUSAL ? 1 : 0);
+  if (h == 0) publish_item(src, item, it);
+}
+
+// dQ = scale * dS K with dS = P (dP - Delta), P = exp(S - LSE), dP = dO V^T;
+// Delta = rowsum(O * dO) is formed here and written out for the dK/dV pass.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
+    const float* __restrict__ dout, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ o, const float* __restrict__ lse,
+    float* __restrict__ delta, float* __restrict__ dq, ItemSource src, int tmax, int head_major,
+    int heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides so,
+    Strides sdq, float scale, int total) {
+  constexpr int DPT = f32_dpt<D>(), TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
+  __shared__ __align__(16) float sK[KT * D];
+  __shared__ __align__(16) float sV[KT * D];
+  const ItemView iv = item_view<false>(src, tmax);
+  if (iv.failed) {
+    poison_rows(dq, sdq, total, heads, D);
+    poison_stats(delta, total, heads);
+    return;
+  }
+  int item, h;
+  if (!map_block(heads, tmax, head_major, group, false, item, h) || item >= iv.count) return;
+  const int4 it = item_at<false>(src, iv, CAUSAL, item);
+  if (it.w == 0) return;
+  const int start = it.z, L = it.w, q0 = it.y * kBM;
+  const int hk = h / group;
+  const int c0 = (threadIdx.x % TPR) * DPT;
+  const float* kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
+  const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
+  const int kend = CAUSAL ? min(L, q0 + kBM) : L;
+  for (int r0 = 0; r0 < kBM && q0 + r0 < L; r0 += RPP) {
+    const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
+    const int64_t tok = start + min(my_q, L - 1);
+    float qv[DPT], dov[DPT], dqv[DPT];
+    float dl;
+    {
+      float ov[DPT];
+      load_slice(qv, q + tok * sq.row + (int64_t)h * sq.head + c0);
+      load_slice(dov, dout + tok * sdo.row + (int64_t)h * sdo.head + c0);
+      load_slice(ov, o + tok * so.row + (int64_t)h * so.head + c0);
+      dl = row_sum<TPR>(dot_slice(ov, dov));
+    }
+    if (my_q < L && c0 == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
+    const float lse2 = lse[tok * heads + h] * kLog2e;
+    const float c = scale * kLog2e;
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) dqv[d] = 0.f;
+    const int qlim = CAUSAL ? min(my_q, L - 1) : L - 1;
+    const int kpass = CAUSAL ? min(kend, q0 + r0 + RPP) : kend;
+    for (int kb = 0; kb < kpass; kb += KT) {
+      __syncthreads();
+      stage_rows_f32<D>(sK, kh, sk.row, kb, kend);
+      stage_rows_f32<D>(sV, vh, sv.row, kb, kend);
+      __syncthreads();
+      float dqt[DPT];
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) dqt[d] = 0.f;
+#pragma unroll 2
+      for (int i = 0; i < KT; ++i) {
+        float kr[DPT], vr[DPT];
+        load_slice(kr, sK + i * D + c0);
+        load_slice(vr, sV + i * D + c0);
+        const float sdot = row_sum<TPR>(dot_slice(qv, kr));
+        const float pdot = row_sum<TPR>(dot_slice(dov, vr));
+        const float p = kb + i <= qlim ? fast_exp2(fmaf(sdot, c, -lse2)) : 0.f;
+        axpy_slice(dqt, p * (pdot - dl), kr);
+      }
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) dqv[d] += dqt[d];
+    }
+    if (my_q < L)
+      store_slice(dq + (int64_t)(start + my_q) * sdq.row + (int64_t)h * sdq.head + c0, dqv, scale);
+  }
+}
+
+// dV = P^T dO and dK = scale * dS^T Q for an item's 128 keys, summed over
+// the query heads that share their K/V head.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dkv_f32_kernel(
+    const float* __restrict__ dout, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
+    float* __restrict__ dk, float* __restrict__ dv, ItemSource src, int tmax, int head_major,
+    int kv_heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk,
+    Strides sdv, float scale, int total) {
+  constexpr int DPT = f32_dpt<D>(), TPR = f32_tpr<D>(), RPP = f32_rows<D>(), QT = kF32Rows;
+  __shared__ __align__(16) float sQ[QT * D];
+  __shared__ __align__(16) float sO[QT * D];  // dO rows
+  __shared__ float sL[QT], sD[QT];             // LSE * log2(e) and Delta of those rows
+  const ItemView iv = item_view<false>(src, tmax);
+  if (iv.failed) {
+    poison_rows(dk, sdk, total, kv_heads, D);
+    poison_rows(dv, sdv, total, kv_heads, D);
+    return;
+  }
+  int item, hk;
+  if (!map_block(kv_heads, tmax, head_major, 1, false, item, hk) || item >= iv.count) return;
+  const int4 it = item_at<false>(src, iv, CAUSAL, item);
+  if (it.w == 0) return;
+  const int start = it.z, L = it.w;
+  const int heads = kv_heads * group;
+  const int nblk = (L + kBM - 1) / kBM;
+  const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
+  const int c0 = (threadIdx.x % TPR) * DPT;
+  const float c = scale * kLog2e;
+  for (int r0 = 0; r0 < kBM && k0 + r0 < L; r0 += RPP) {
+    const int my_k = k0 + r0 + (int)threadIdx.x / TPR;
+    const int64_t tok = start + min(my_k, L - 1);
+    float kv[DPT], vv[DPT], dkv[DPT], dvv[DPT];
+    load_slice(kv, k + tok * sk.row + (int64_t)hk * sk.head + c0);
+    load_slice(vv, v + tok * sv.row + (int64_t)hk * sv.head + c0);
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) dkv[d] = dvv[d] = 0.f;
+    const int qbeg = CAUSAL ? k0 + r0 : 0;  // no earlier query sees this pass's keys
+    for (int gi = 0; gi < group; ++gi) {
+      const int h = hk * group + gi;
+      const float* qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
+      const float* dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
+      for (int qb = qbeg; qb < L; qb += QT) {
+        __syncthreads();
+        stage_rows_f32<D>(sQ, qh, sq.row, qb, L);
+        stage_rows_f32<D>(sO, dh, sdo.row, qb, L);
+        if (threadIdx.x < QT) {
+          const int qq = qb + (int)threadIdx.x;
+          sL[threadIdx.x] = qq < L ? lse[(int64_t)(start + qq) * heads + h] * kLog2e : 0.f;
+          sD[threadIdx.x] = qq < L ? delta[(int64_t)(start + qq) * heads + h] : 0.f;
+        }
+        __syncthreads();
+        float dkt[DPT], dvt[DPT];
+#pragma unroll
+        for (int d = 0; d < DPT; ++d) dkt[d] = dvt[d] = 0.f;
+#pragma unroll 2
+        for (int i = 0; i < QT; ++i) {
+          const int qq = qb + i;
+          float qr[DPT], orow[DPT];
+          load_slice(qr, sQ + i * D + c0);
+          load_slice(orow, sO + i * D + c0);
+          const float sdot = row_sum<TPR>(dot_slice(kv, qr));
+          const float pdot = row_sum<TPR>(dot_slice(vv, orow));
+          const bool ok = qq < L && (!CAUSAL || qq >= my_k);
+          const float p = ok ? fast_exp2(fmaf(sdot, c, -sL[i])) : 0.f;
+          axpy_slice(dvt, p, orow);
+          axpy_slice(dkt, p * (pdot - sD[i]), qr);
+        }
+#pragma unroll
+        for (int d = 0; d < DPT; ++d) {
+          dkv[d] += dkt[d];
+          dvv[d] += dvt[d];
+        }
+      }
+    }
+    if (my_k < L) {
+      store_slice(dk + (int64_t)(start + my_k) * sdk.row + (int64_t)hk * sdk.head + c0, dkv, scale);
+      store_slice(dv + (int64_t)(start + my_k) * sdv.row + (int64_t)hk * sdv.head + c0, dvv, 1.0f);
+    }
+  }
+}
+
 // ------------------------------------------------------------------- host
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -1927,8 +2251,8 @@ int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, in
   if (!head_dim_supported(head_dim))
     return set_error(SCREE_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (16, 32, 64, 128, 256)",
                      fn, head_dim);
-  if (dtype != SCREE_DTYPE_F16 && dtype != SCREE_DTYPE_BF16)
-    return set_error(SCREE_ERR_UNSUPPORTED, "%s: dtype code %d unsupported (fp16 / bf16 only)", fn,
+  if (dtype != SCREE_DTYPE_F16 && dtype != SCREE_DTYPE_BF16 && dtype != SCREE_DTYPE_F32)
+    return set_error(SCREE_ERR_UNSUPPORTED, "%s: dtype code %d unsupported (fp16, bf16, fp32)", fn,
                      dtype);
   const size_t need = scree_attn_workspace_bytes(batch, total, head_dim);
   if (!workspace || workspace_bytes < need)
@@ -2090,6 +2414,66 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
       SCREE_DISPATCH_T(FN, bf16, D, causal, __VA_ARGS__);                         \
   } while (0)
 
+// fp32 kernels: FN<head_dim, causal>(...), every head_dim natively.
+#define SCREE_DISPATCH_F32(FN, D, causal, ...)                                                   \
+  do {                                                                                           \
+    if (D == 16) { if (causal) FN<16, true>(__VA_ARGS__); else FN<16, false>(__VA_ARGS__); }     \
+    else if (D == 32) { if (causal) FN<32, true>(__VA_ARGS__); else FN<32, false>(__VA_ARGS__); } \
+    else if (D == 64) { if (causal) FN<64, true>(__VA_ARGS__); else FN<64, false>(__VA_ARGS__); } \
+    else if (D == 128) { if (causal) FN<128, true>(__VA_ARGS__); else FN<128, false>(__VA_ARGS__); } \
+    else { if (causal) FN<256, true>(__VA_ARGS__); else FN<256, false>(__VA_ARGS__); }           \
+  } while (0)
+
+template <int D, bool C>
+void launch_fwd_f32(const void* q, const void* k, const void* v, void* o, float* lse,
+                    const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
+                    float scale, int tmax, void* ws, int total, hipStream_t stream) {
+  const int64_t grid = (int64_t)tmax * heads;
+  const int hm = attn_head_major(heads, tmax);
+  hipLaunchKernelGGL((attn_fwd_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()), 0,
+                     stream, static_cast<const float*>(q), static_cast<const float*>(k),
+                     static_cast<const float*>(v), static_cast<float*>(o), lse,
+                     fwd_item_source(ws, cu, batch, total, tmax, heads, D, hm), tmax, hm, heads,
+                     heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
+                     Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, total);
+}
+
+// strides: {dout, q, k, v, o, dq} x {row, head}
+template <int D, bool C>
+void launch_bwd_dq_f32(const void* dout, const void* q, const void* k, const void* v,
+                       const void* o, const float* lse, void* dq, float* delta, int heads,
+                       int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
+                       int total, hipStream_t stream) {
+  const int64_t grid = (int64_t)tmax * heads;
+  const int hm = attn_head_major(heads, tmax);
+  hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()),
+                     0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
+                     static_cast<const float*>(k), static_cast<const float*>(v),
+                     static_cast<const float*>(o), lse, delta, static_cast<float*>(dq),
+                     list_item_source(ws, total, tmax, hm), tmax, hm, heads, heads / kv_heads,
+                     Strides{st[0], st[1]}, Strides{st[2], st[3]}, Strides{st[4], st[5]},
+                     Strides{st[6], st[7]}, Strides{st[8], st[9]}, Strides{st[10], st[11]}, scale,
+                     total);
+}
+
+// strides: {dout, q, k, v, dk, dv} x {row, head}; one workgroup per (item, K/V head)
+template <int D, bool C>
+void launch_bwd_dkv_f32(const void* dout, const void* q, const void* k, const void* v,
+                        const float* lse, const float* delta, void* dk, void* dv, int heads,
+                        int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
+                        int total, hipStream_t stream) {
+  const int64_t grid = (int64_t)tmax * kv_heads;
+  const int hm = attn_head_major(kv_heads, tmax);
+  hipLaunchKernelGGL((attn_bwd_dkv_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()),
+                     0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
+                     static_cast<const float*>(k), static_cast<const float*>(v), lse, delta,
+                     static_cast<float*>(dk), static_cast<float*>(dv),
+                     list_item_source(ws, total, tmax, hm), tmax, hm, kv_heads,
+                     heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
+                     Strides{st[4], st[5]}, Strides{st[6], st[7]}, Strides{st[8], st[9]},
+                     Strides{st[10], st[11]}, scale, total);
+}
+
 }  // namespace
 }  // namespace scree
 
@@ -2189,9 +2573,14 @@ static int launch_fwd(const char* fn, const void* q, const void* k, const void* 
                       void* stream) {
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
-  SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, batch, heads,
-                 kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens, head_dim,
-                 static_cast<hipStream_t>(stream));
+  if (dtype == SCREE_DTYPE_F32)
+    SCREE_DISPATCH_F32(launch_fwd_f32, head_dim, causal, q, k, v, o, lse, cu_seqlens, batch, heads,
+                       kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens,
+                       static_cast<hipStream_t>(stream));
+  else
+    SCREE_DISPATCH(launch_fwd_t, dtype, head_dim, causal, q, k, v, o, lse, cu_seqlens, batch,
+                   heads, kv_heads, strides, softmax_scale, tmax, workspace, (int)total_tokens,
+                   head_dim, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
@@ -2307,9 +2696,14 @@ extern "C" int scree_attn_bwd_dq_gqa(const void* dout, const void* q, const void
   if (rc) return rc;
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
-  SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
-                 cu_seqlens, batch, heads, kv_heads, strides, softmax_scale, tmax, workspace,
-                 (int)total_tokens, head_dim, static_cast<hipStream_t>(stream));
+  if (dtype == SCREE_DTYPE_F32)
+    SCREE_DISPATCH_F32(launch_bwd_dq_f32, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
+                       heads, kv_heads, strides, softmax_scale, tmax, workspace,
+                       (int)total_tokens, static_cast<hipStream_t>(stream));
+  else
+    SCREE_DISPATCH(launch_bwd_dq_t, dtype, head_dim, causal, dout, q, k, v, o, lse, dq, delta,
+                   cu_seqlens, batch, heads, kv_heads, strides, softmax_scale, tmax, workspace,
+                   (int)total_tokens, head_dim, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
@@ -2345,6 +2739,12 @@ extern "C" int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const voi
   if (rc) return rc;
   if (total_tokens == 0) return SCREE_OK;
   const int tmax = (int)tmax_for(batch, total_tokens);
+  if (dtype == SCREE_DTYPE_F32) {  // one workgroup per (item, K/V head), no split
+    SCREE_DISPATCH_F32(launch_bwd_dkv_f32, head_dim, causal, dout, q, k, v, lse, delta, dk, dv,
+                       heads, kv_heads, strides, softmax_scale, tmax, workspace,
+                       (int)total_tokens, static_cast<hipStream_t>(stream));
+    return check_launch(fn);
+  }
   // Split the head groups only when the caller's workspace has room for it
   // (scree_attn_bwd_workspace_bytes_gqa); otherwise one part per group.
   int gsplit = dkv_gsplit(tmax, kv_heads, heads / kv_heads);

@@ -37,28 +37,30 @@ def varlen_attention(q: Array, k: Array, v: Array, causal: bool = False) -> Arra
     only the two ends) make every output and gradient NaN: the device
     scheduler checks them, so no host read of the offsets is needed.
 
-    Values must be fp16 or bf16, the types the kernels' matrix instructions
-    take, as for the reference's Triton launcher
-    (``triton/varlen_attention.py:215``).  The reference's Array-level torch
-    branch also runs fp32 (``reference/varlen_attention.py:90-113``); here
-    fp32 (or any other dtype) raises ``TypeError`` rather than being computed
-    at a lower precision than the caller asked for.
+    Values may be fp16 or bf16 (the matrix-instruction kernels, as the
+    reference's Triton launcher takes, ``triton/varlen_attention.py:215``) or
+    fp32, which the reference's Array-level torch branch also computes
+    (``reference/varlen_attention.py:90-113``): fp32 runs on kernels that
+    keep every operand in fp32.  q, k and v must share the dtype; any other
+    dtype raises ``TypeError``.  The result supports autograd in every case.
     """
     import torch
 
-    from .hip import varlen_attention_hip_autograd
+    from .hip import VarlenAttentionHip
 
     _require_device(q.values, "varlen_attention")
     for name, a in (("q", q), ("k", k), ("v", v)):
-        if a.values.dtype not in (torch.float16, torch.bfloat16):
+        if a.values.dtype not in (torch.float16, torch.bfloat16, torch.float32):
             raise TypeError(f"varlen_attention: {name} is {a.values.dtype}; the HIP kernels take "
-                            "float16 or bfloat16 (cast with .half() or .bfloat16())")
+                            "float16, bfloat16 or float32")
+    if not (q.values.dtype == k.values.dtype == v.values.dtype):
+        raise TypeError("varlen_attention: q, k and v must share a dtype")
     if not (q.offsets is k.offsets and q.offsets is v.offsets):
         if not (torch.equal(q.offsets, k.offsets) and torch.equal(q.offsets, v.offsets)):
             raise ValueError("q, k, v must have identical offsets")
     if q.ragged_dim != 0:
         raise NotImplementedError("varlen_attention supports ragged_dim=0 only")
-    out = varlen_attention_hip_autograd(q.values, k.values, v.values, q.offsets, causal)
+    out = VarlenAttentionHip.apply(q.values, k.values, v.values, q.offsets, causal)
     return Array._trusted(out, q.offsets, 0)
 
 

@@ -25,7 +25,7 @@ from . import attention as _attn
 class VarlenAttentionHip(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, cu_seqlens, causal):
-        _attn._check_inputs(q, k, v)
+        _attn._check_inputs(q, k, v, allow_fp32=True)
         total, n_heads, head_dim = q.shape
         cu = _attn._cu(cu_seqlens, q.device)
         qk, kk, vk = _attn._kernel_view(q), _attn._kernel_view(k), _attn._kernel_view(v)
@@ -58,5 +58,10 @@ class VarlenAttentionHip(torch.autograd.Function):
 
 
 def varlen_attention_hip_autograd(q, k, v, cu_seqlens, causal: bool = False):
-    """Autograd-aware varlen attention; ``out.backward()`` runs the HIP backward."""
+    """Autograd-aware varlen attention; ``out.backward()`` runs the HIP backward.
+
+    fp16 / bf16, as the reference's Triton autograd (its launcher asserts
+    them); the Array-level ``scree_amd.kernels.varlen_attention`` applies
+    :class:`VarlenAttentionHip` to fp32 values as well."""
+    _attn._check_inputs(q, k, v)
     return VarlenAttentionHip.apply(q, k, v, cu_seqlens, causal)

@@ -35,7 +35,10 @@ import torch
 from . import _ffi
 
 
-def _check_inputs(q, k, v):
+def _check_inputs(q, k, v, allow_fp32: bool = False):
+    """The launchers' checks (``triton/varlen_attention.py:213-215``): fp16 or
+    bf16, as the reference's GPU launchers; ``allow_fp32`` for the
+    Array-level path, which also takes fp32 (computed by the fp32 kernels)."""
     assert k.shape == v.shape, "k and v must have identical shape"
     assert q.dim() == 3 and k.dim() == 3, "q, k, v must be (total_tokens, n_heads, head_dim)"
     assert q.shape[0] == k.shape[0] and q.shape[2] == k.shape[2], (
@@ -43,7 +46,9 @@ def _check_inputs(q, k, v):
     assert k.shape[1] >= 1 and q.shape[1] % k.shape[1] == 0, (
         "k/v heads must divide q heads (grouped-query attention)")
     assert q.is_cuda, "varlen_attention_hip requires ROCm device tensors"
-    assert q.dtype in (torch.float16, torch.bfloat16), "fp16 or bf16 only"
+    dtypes = (torch.float16, torch.bfloat16, torch.float32) if allow_fp32 else (torch.float16,
+                                                                               torch.bfloat16)
+    assert q.dtype in dtypes, "fp16 or bf16 only" if not allow_fp32 else "fp16, bf16 or fp32 only"
     assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
     assert q.dim() == 3, "q, k, v must be (total_tokens, n_heads, head_dim)"
 

@@ -4,7 +4,9 @@ Tolerances (north star): attention outputs within 2e-3 and dq/dk/dv within
 5e-3 max-abs of an fp32-or-better reference, norms within 1e-3 (half) and 1e-5
 (fp32).  The reference is the oracle evaluated in fp64 on the *same rounded
 inputs* the GPU sees.  fp16 attention at ordinary logits uses the flat bounds
-unchanged.
+unchanged.  fp32 attention (the Array-level path) is held to 1e-5, the
+reference's own fp32 bound, plus the same two terms with ``u = 2^-24`` and
+``E_ref`` from the reference's fp32 arithmetic.
 
 bf16 keeps 8 significant bits: rounding the stored result alone can exceed
 the flat bounds, and so can rounding P and dS before their dots, which the
@@ -84,16 +86,27 @@ def reference_excess(q, k, v, do, off, causal, dtype, o=None, lse=None):
     from oracle.attention import (attention_bwd, attention_bwd_rounded, attention_fwd,
                                   attention_fwd_rounded)
 
-    operand = {torch.float16: "float16", torch.bfloat16: "bfloat16"}[dtype]
     u = UNIT[dtype]
     ro, rl = attention_fwd(q, k, v, off, causal=causal)
-    eo, el = attention_fwd_rounded(q, k, v, off, causal=causal, operand=operand)
+    if dtype == torch.float32:
+        # the reference's Array-level fp32 path: the same sums as GEMMs in
+        # fp32 arithmetic (reference/varlen_attention.py:90-113)
+        eo, el = attention_fwd(q, k, v, off, causal=causal, dtype=np.float32)
+
+        def emulate(bo, bl):
+            return attention_bwd(do, q, k, v, bo, bl, off, causal=causal, dtype=np.float32)[:3]
+    else:
+        operand = {torch.float16: "float16", torch.bfloat16: "bfloat16"}[dtype]
+        eo, el = attention_fwd_rounded(q, k, v, off, causal=causal, operand=operand)
+
+        def emulate(bo, bl):
+            return attention_bwd_rounded(do, q, k, v, bo, bl, off, causal=causal, operand=operand)
     ex = lambda got, ref: max(0.0, float((np.abs(got - ref) - u * np.abs(ref)).max()))  # noqa: E731
     out = {"O": ex(eo, ro)}
     if do is not None:
         bo = eo if o is None else o
         bl = el if lse is None else lse
-        emul = attention_bwd_rounded(do, q, k, v, bo, bl, off, causal=causal, operand=operand)
+        emul = emulate(bo, bl)
         exact = attention_bwd(do, q, k, v, bo, rl, off, causal=causal)
         for name, a, b in zip(("dQ", "dK", "dV"), emul, exact):
             out[name] = ex(a, b)

@@ -51,8 +51,8 @@ def test_attention_validation_errors():
         rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, bad_dim, strides, 0.125, 1, 1, p,
                                 1 << 16, null)
         assert rc == _ffi.SCREE_ERR_UNSUPPORTED and "head_dim" in _err()
-    # fp32 is not an attention dtype
-    rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 64, strides, 0.125, 1, 0, p, 1 << 16, null)
+    # dtype codes other than fp32 / fp16 / bf16
+    rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 64, strides, 0.125, 1, 7, p, 1 << 16, null)
     assert rc == _ffi.SCREE_ERR_UNSUPPORTED and "dtype" in _err()
     # workspace too small
     rc = lib.scree_attn_fwd(p, p, p, p, p, p, 2, 10, 16, 64, strides, 0.125, 1, 1, p, 8, null)

@@ -6,8 +6,9 @@ seed 0; 1,980 tokens), 4 heads of head_dim 32, causal and non-causal
 attention; RMSNorm with gamma = 1 on the same packed tensor viewed as
 (1980, 4, 32) and on a (1980, 128) tensor.  The reference runs attention in
 fp32 on the CPU; its GPU launchers (and these) take fp16 / bf16, so attention
-runs in both half types against the fp64 oracle on the same rounded inputs.
-RMSNorm runs in fp32 with the 1e-5 bound.
+runs in both half types against the fp64 oracle on the same rounded inputs,
+and in fp32 through the Array-level call (the fp32 kernels) with the 1e-5
+bound.  RMSNorm runs in fp32 with the 1e-5 bound.
 
 Also here: the reference's launcher names bound to the HIP launchers, a
 schedule that fails on overlapping offsets (outputs NaN, never stale
@@ -34,19 +35,37 @@ def test_config1_attention_fwd_bwd(dtype, causal):
     _run_case(lengths, 4, 32, dtype, causal, seed=1, backward=True)
 
 
-def test_config1_fp32_attention_raises_type_error():
-    """Config 1 is stated in fp32.  The Array-level call takes only the half
-    types the kernels compute in and says so, instead of computing fp32
-    inputs at a lower precision."""
+@pytest.mark.parametrize("causal", [True, False])
+def test_config1_fp32_attention_fwd_bwd(causal):
+    """Config 1 as stated: fp32, through the Array-level call (the fp32
+    kernels) with autograd, within the reference's fp32 bound of 1e-5."""
+    from test_gpu_attention_fp32 import run_fp32_case
+
+    lengths = workloads.config1_lengths()
+    run_fp32_case(lengths, 4, 32, causal, seed=3)
+
+
+def test_attention_rejects_other_dtypes():
+    """fp64 (or mixed dtypes) raise TypeError at the Array level; the
+    reference-named launchers keep their fp16 / bf16 assertion."""
     import scree_amd
     from scree_amd.kernels import varlen_attention
+    from scree_amd.kernels.hip import varlen_attention_triton, varlen_attention_triton_autograd
 
-    say("case: config1 fp32 Array-level attention -> TypeError")
-    lengths = workloads.config1_lengths()
+    say("case: fp64 / mixed-dtype Array-level attention -> TypeError")
+    lengths = [5, 9]
     _, cu = cu_of(lengths)
-    x = scree_amd.Array(values=randn((sum(lengths), 4, 32), torch.float32, 2), offsets=cu)
-    with pytest.raises(TypeError, match="float16 or bfloat16"):
-        varlen_attention(x, x, x, causal=True)
+    x64 = scree_amd.Array(values=randn((14, 2, 32), torch.float64, 2), offsets=cu)
+    with pytest.raises(TypeError, match="float32"):
+        varlen_attention(x64, x64, x64, causal=True)
+    x32 = scree_amd.Array(values=randn((14, 2, 32), torch.float32, 3), offsets=cu)
+    x16 = scree_amd.Array(values=randn((14, 2, 32), torch.float16, 4), offsets=cu)
+    with pytest.raises(TypeError, match="share a dtype"):
+        varlen_attention(x32, x16, x16, causal=True)
+    with pytest.raises(AssertionError, match="fp16 or bf16"):
+        varlen_attention_triton(x32.values, x32.values, x32.values, cu)
+    with pytest.raises(AssertionError, match="fp16 or bf16"):
+        varlen_attention_triton_autograd(x32.values, x32.values, x32.values, cu)
 
 
 @pytest.mark.parametrize("shape", [(1980, 4, 32), (1980, 128)])
