@@ -348,11 +348,13 @@ def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup):
 def time_config1_gpu(steps, warmup):
     """Config 1 (the reference's CPU plumbing case) on the GPU path.
 
-    Config 1 is stated in fp32, which the reference's GPU launcher rejects
-    (``triton/varlen_attention.py:215``: fp16/bf16 only), so attention runs
-    in fp16 on the same lengths and 4 heads x head_dim 32 (causal, forward
-    and forward+backward); RMSNorm runs in fp32 on the packed tokens as
-    (tokens, 128) rows with gamma = 1, the reference's own reshaping
+    Config 1 is stated in fp32: attention runs in fp32 on the fp32 kernels
+    (what the Array-level call takes fp32 arrays to; the reference's GPU
+    launcher rejects fp32, ``triton/varlen_attention.py:215``) and, for
+    comparison, in fp16 on the matrix-instruction kernels, on the same
+    lengths and 4 heads x head_dim 32 (causal, forward and forward+backward);
+    RMSNorm runs in fp32 on the packed tokens as (tokens, 128) rows with
+    gamma = 1, the reference's own reshaping
     (``benchmarks/bench_throughput.py:122``).
     """
     import torch
@@ -362,11 +364,12 @@ def time_config1_gpu(steps, warmup):
 
     lengths = workloads.config1_lengths()
     out = {"tokens": int(sum(lengths))}
-    for bwd in (False, True):
-        cfg = workloads.AttnConfig("cfg1_attn_gpu", lengths, 4, 32, "fp16", True, bwd)
-        r, _ = time_attention(cfg, torch.float16, steps, warmup, backward=bwd)
-        out["attn_causal_fp16_fwd_bwd" if bwd else "attn_causal_fp16_fwd"] = {
-            "us": round(r["ms"] * 1e3, 2), "tflops": round(r["tflops"], 3)}
+    for name, dt in (("fp32", torch.float32), ("fp16", torch.float16)):
+        for bwd in (False, True):
+            cfg = workloads.AttnConfig("cfg1_attn_gpu", lengths, 4, 32, name, True, bwd)
+            r, _ = time_attention(cfg, dt, steps, warmup, backward=bwd)
+            out[f"attn_causal_{name}_fwd_bwd" if bwd else f"attn_causal_{name}_fwd"] = {
+                "us": round(r["ms"] * 1e3, 2), "tflops": round(r["tflops"], 3)}
     dev = torch.device("cuda:0")
     x = torch.randn(out["tokens"], 128, device=dev, dtype=torch.float32,
                     generator=torch.Generator(device=dev).manual_seed(3))
