@@ -747,9 +747,8 @@ constexpr int kXcds = 8;
 // blocks 2k and 2k + 1 run as blocks b and b + 8 of each group of 16, which
 // share an XCD and its L2 (block b runs on XCD b mod 8); blocks past the last
 // full group of 16 keep their index.
-__device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, int group,
-                                          bool pair, int& item, int& head) {
-  int b = blockIdx.x;
+__device__ __forceinline__ bool map_block_at(int b, int heads, int tmax, int head_major, int group,
+                                             bool pair, int& item, int& head) {
   if (head_major) {
     const int x = b % kXcds, j = b / kXcds;
     const int k = j / tmax;  // k-th head of this XCD
@@ -763,6 +762,10 @@ __device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, i
   }
   if (group > 1 && heads % kXcds == 0) head = (head % kXcds) * (heads / kXcds) + head / kXcds;
   return true;
+}
+__device__ __forceinline__ bool map_block(int heads, int tmax, int head_major, int group,
+                                          bool pair, int& item, int& head) {
+  return map_block_at(blockIdx.x, heads, tmax, head_major, group, pair, item, head);
 }
 
 // The scheduler publishes header[1] = -1 when some offset decreases (which is
@@ -1892,43 +1895,50 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
 // fp32 inputs, which the reference's Array-level function computes as given
 // (its torch branch, reference/varlen_attention.py:90-113).  The matrix
 // instructions run fp32 at a sixteenth of their 16-bit rate, so these kernels
-// use FP32 FMAs instead: each row of an item is split over TPR = D / DPT
-// threads (consecutive lanes of one wave) holding DPT consecutive columns, a
-// dot product is DPT FMAs plus a sum over those lanes, and K / V (or Q / dO)
-// rows are staged 32 at a time in LDS, where every row group reads the same
-// staged row (a broadcast).  A workgroup of at most 512 threads covers its
-// item's 128 rows in 128 / RPP passes of RPP rows (2 at head_dim 128, 4 at
-// 256).  Scores, weights, sums and accumulators are fp32; the forward takes
-// each 32-key tile's maximum before forming its weights, so every weight is
-// at most 1, as in the reference's max-subtracted softmax.  Every sum over
-// keys or queries is taken per 32-row tile first and then over the tiles,
-// which keeps its rounding error near that of the blocked sums of a GEMM
-// (a group of 4 heads over 1,000 queries otherwise added 3x the reference's
-// own fp32 error to dV).  Same work lists, item order and failure handling
-// as the 16-bit kernels.
-template <int D>
-constexpr int f32_dpt() {
-  return 16;
-}
+// use FP32 FMAs instead: each row of an item (a query, or a key for dK/dV) is
+// split over TPR = D / 16 consecutive lanes holding 16 columns each, a dot
+// product is 16 FMAs plus a DPP sum over those lanes, and K / V (or Q / dO)
+// rows are staged 32 at a time in LDS, where every row group of a wave reads
+// the same staged row (a broadcast); the next 32 rows are loaded into
+// registers while the current ones are used.  Two workgroups share an item,
+// 64 rows each (in passes of 32 rows at head_dim 256), which doubles the
+// workgroups a small problem spreads over the CUs.  Scores, weights, sums and
+// accumulators are fp32; the forward takes each 32-key tile's maximum before
+// forming its weights, so every weight is at most 1, as in the reference's
+// max-subtracted softmax.  Every sum over keys or queries is taken per
+// 32-row tile first and then over the tiles, which keeps its rounding error
+// near that of the blocked sums of a GEMM (a group of 4 heads over 1,000
+// queries otherwise added 3x the reference's own fp32 error to dV).  Same
+// work lists, item order and failure handling as the 16-bit kernels.
+constexpr int kF32Split = 2;                // workgroups per item
+constexpr int kF32WgRows = kBM / kF32Split;  // rows of an item per workgroup
+constexpr int kF32Rows = 32;                // keys (forward, dQ) or queries (dK/dV) per LDS tile
 template <int D>
 constexpr int f32_tpr() {
-  return D / f32_dpt<D>();  // 1 to 16
+  return D / 16;  // lanes per row, 16 columns each
 }
 template <int D>
 constexpr int f32_rows() {
-  return kBM * f32_tpr<D>() <= 512 ? kBM : 512 / f32_tpr<D>();  // rows per pass
+  return kF32WgRows * f32_tpr<D>() <= 512 ? kF32WgRows : 512 / f32_tpr<D>();  // rows per pass
 }
 template <int D>
 constexpr int f32_threads() {
   return f32_rows<D>() * f32_tpr<D>();
 }
-constexpr int kF32Rows = 32;  // keys (forward, dQ) or queries (dK/dV) per LDS tile
 
-// Sum over the TPR consecutive lanes of one row (TPR divides 64).
+// Sum over the TPR (1 to 16) consecutive lanes of one row, by the DPP steps
+// of wave_sum_i (lane ^ 1, lane ^ 2, then the mirrors across 8 and 16
+// lanes): VALU operations, no LDS round trip per reduction.
 template <int TPR>
 __device__ __forceinline__ float row_sum(float x) {
-#pragma unroll
-  for (int m = 1; m < TPR; m <<= 1) x += __shfl_xor(x, m, kWave);
+  static_assert(TPR >= 1 && TPR <= 16 && (TPR & (TPR - 1)) == 0, "TPR: a power of two <= 16");
+  auto step = [](float v, auto ctrl) {
+    return v + __builtin_bit_cast(float, dpp_i<decltype(ctrl)::value>(__builtin_bit_cast(int, v)));
+  };
+  if constexpr (TPR >= 2) x = step(x, std::integral_constant<int, 0xB1>{});
+  if constexpr (TPR >= 4) x = step(x, std::integral_constant<int, 0x4E>{});
+  if constexpr (TPR >= 8) x = step(x, std::integral_constant<int, 0x141>{});
+  if constexpr (TPR >= 16) x = step(x, std::integral_constant<int, 0x140>{});
   return x;
 }
 template <int N>
@@ -1961,27 +1971,45 @@ __device__ __forceinline__ void axpy_slice(float (&acc)[N], float a, const float
 #pragma unroll
   for (int i = 0; i < N; ++i) acc[i] = fmaf(a, x[i], acc[i]);
 }
-// Rows [row0, row0 + kF32Rows) of a head's (tokens, D) rows at `base` into
-// `lds` (row-major, D floats per row); rows >= limit become zeros.
-template <int D>
-__device__ __forceinline__ void stage_rows_f32(float* lds, const float* __restrict__ base,
-                                               int64_t row_stride, int row0, int limit) {
-  constexpr int C4 = D / 4;
-  for (int idx = threadIdx.x; idx < kF32Rows * C4; idx += blockDim.x) {
-    const int r = idx / C4, c = 4 * (idx % C4);
-    const int row = row0 + r;
-    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < limit) t = *reinterpret_cast<const float4*>(base + (int64_t)row * row_stride + c);
-    *reinterpret_cast<float4*>(lds + r * D + c) = t;
+
+// Two (rows, D) matrices' rows [row0, row0 + kF32Rows) through registers into
+// LDS (row-major, D floats per row); rows >= limit become zeros.  load()
+// issues the global reads, store() writes what they returned.
+template <int D, int THREADS>
+struct F32Stage {
+  static constexpr int C4 = D / 4;
+  static constexpr int N4 = kF32Rows * C4;  // float4 per matrix
+  static constexpr int PER = (N4 + THREADS - 1) / THREADS;
+  float4 a[PER], b[PER];
+  __device__ __forceinline__ void load(const float* __restrict__ pa, int64_t sa,
+                                       const float* __restrict__ pb, int64_t sb, int row0, int limit) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int idx = (int)threadIdx.x + j * THREADS;
+      const int r = idx / C4, c = 4 * (idx % C4), row = row0 + r;
+      const bool ok = idx < N4 && row < limit;
+      a[j] = ok ? *reinterpret_cast<const float4*>(pa + (int64_t)row * sa + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      b[j] = ok ? *reinterpret_cast<const float4*>(pb + (int64_t)row * sb + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
-}
+  __device__ __forceinline__ void store(float* la, float* lb) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int idx = (int)threadIdx.x + j * THREADS;
+      if (idx < N4) {
+        reinterpret_cast<float4*>(la)[idx] = a[j];
+        reinterpret_cast<float4*>(lb)[idx] = b[j];
+      }
+    }
+  }
+};
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(f32_threads<D>()) void attn_fwd_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ lse, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sq, Strides sk, Strides sv, Strides so, float scale, int total) {
-  constexpr int DPT = f32_dpt<D>(), TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
+  constexpr int DPT = 16, TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
   const ItemView iv = item_view<true>(src, tmax);
@@ -1991,70 +2019,75 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_fwd_f32_kernel(
     poison_stats(lse, total, heads);
     return;
   }
+  const int part = blockIdx.x % kF32Split;
   int item, h;
-  if (!map_block(heads, tmax, head_major, group, false, item, h) || item >= iv.count) {
+  if (!map_block_at(blockIdx.x / kF32Split, heads, tmax, head_major, group, false, item, h) ||
+      item >= iv.count) {
     publish_header(src, iv, CAUSAL ? 1 : 0);
     return;
   }
   const int4 it = item_at<true>(src, iv, CAUSAL, item);
-  if (it.w == 0) return;
-  const int start = it.z, L = it.w, q0 = it.y * kBM;
-  const int hk = h / group;
-  const int c0 = (threadIdx.x % TPR) * DPT;
-  const float* kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
-  const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
-  const int kend = CAUSAL ? min(L, q0 + kBM) : L;
-  for (int r0 = 0; r0 < kBM && q0 + r0 < L; r0 += RPP) {
-    const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
-    // rows past L compute on row L-1 and store nothing
-    float qv[DPT], ov[DPT];
-    load_slice(qv, q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head + c0);
+  const int start = it.z, L = it.w, q0 = it.y * kBM + part * kF32WgRows;  // this workgroup's rows
+  if (L > 0 && q0 < L) {
+    const int hk = h / group;
+    const int c0 = (threadIdx.x % TPR) * DPT;
+    const float* kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
+    const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
+    const int kend = CAUSAL ? min(L, q0 + kF32WgRows) : L;
+    F32Stage<D, f32_threads<D>()> stage;
+    for (int r0 = 0; r0 < kF32WgRows && q0 + r0 < L; r0 += RPP) {
+      const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
+      // rows past L compute on row L-1 and store nothing
+      float qv[DPT], ov[DPT];
+      load_slice(qv, q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head + c0);
 #pragma unroll
-    for (int i = 0; i < DPT; ++i) ov[i] = 0.f;
-    float m = kNegInf, l = 0.f;
-    const int qlim = CAUSAL ? min(my_q, L - 1) : L - 1;  // the last key this row sees
-    const int kpass = CAUSAL ? min(kend, q0 + r0 + RPP) : kend;
-    for (int kb = 0; kb < kpass; kb += KT) {
-      __syncthreads();  // the previous tile is consumed
-      stage_rows_f32<D>(sK, kh, sk.row, kb, kend);
-      stage_rows_f32<D>(sV, vh, sv.row, kb, kend);
-      __syncthreads();
-      float s[KT];
-      float tile_m = kNegInf;
+      for (int i = 0; i < DPT; ++i) ov[i] = 0.f;
+      float m = kNegInf, l = 0.f;
+      const int qlim = CAUSAL ? min(my_q, L - 1) : L - 1;  // the last key this row sees
+      const int kpass = CAUSAL ? min(kend, q0 + r0 + RPP) : kend;
+      stage.load(kh, sk.row, vh, sv.row, 0, kend);
+      for (int kb = 0; kb < kpass; kb += KT) {
+        __syncthreads();  // the previous tile is consumed
+        stage.store(sK, sV);
+        __syncthreads();
+        if (kb + KT < kpass) stage.load(kh, sk.row, vh, sv.row, kb + KT, kend);
+        float s[KT];
+        float tile_m = kNegInf;
 #pragma unroll
-      for (int i = 0; i < KT; ++i) {
-        float kr[DPT];
-        load_slice(kr, sK + i * D + c0);
-        const float dotv = row_sum<TPR>(dot_slice(qv, kr)) * scale;
-        s[i] = kb + i <= qlim ? dotv : kNegInf;
-        tile_m = fmaxf(tile_m, s[i]);
-      }
-      // key 0 is in every row's first tile, so m is finite from then on
-      const float m_new = fmaxf(m, tile_m);
-      const float alpha = fast_exp2((m - m_new) * kLog2e);
-      float ot[DPT], lt = 0.f;
+        for (int i = 0; i < KT; ++i) {
+          float kr[DPT];
+          load_slice(kr, sK + i * D + c0);
+          const float dotv = row_sum<TPR>(dot_slice(qv, kr)) * scale;
+          s[i] = kb + i <= qlim ? dotv : kNegInf;
+          tile_m = fmaxf(tile_m, s[i]);
+        }
+        // key 0 is in every row's first tile, so m is finite from then on
+        const float m_new = fmaxf(m, tile_m);
+        const float alpha = fast_exp2((m - m_new) * kLog2e);
+        float ot[DPT], lt = 0.f;
 #pragma unroll
-      for (int d = 0; d < DPT; ++d) ot[d] = 0.f;
+        for (int d = 0; d < DPT; ++d) ot[d] = 0.f;
 #pragma unroll 4
-      for (int i = 0; i < KT; ++i) {
-        const float p = fast_exp2((s[i] - m_new) * kLog2e);
-        float vr[DPT];
-        load_slice(vr, sV + i * D + c0);
-        lt += p;
-        axpy_slice(ot, p, vr);
-      }
-      l = fmaf(l, alpha, lt);
+        for (int i = 0; i < KT; ++i) {
+          const float p = fast_exp2((s[i] - m_new) * kLog2e);
+          float vr[DPT];
+          load_slice(vr, sV + i * D + c0);
+          lt += p;
+          axpy_slice(ot, p, vr);
+        }
+        l = fmaf(l, alpha, lt);
 #pragma unroll
-      for (int d = 0; d < DPT; ++d) ov[d] = fmaf(ov[d], alpha, ot[d]);
-      m = m_new;
-    }
-    if (my_q < L) {
-      store_slice(o + (int64_t)(start + my_q) * so.row + (int64_t)h * so.head + c0, ov, 1.0f / l);
-      if (c0 == 0) lse[(int64_t)(start + my_q) * heads + h] = m + logf(l);
+        for (int d = 0; d < DPT; ++d) ov[d] = fmaf(ov[d], alpha, ot[d]);
+        m = m_new;
+      }
+      if (my_q < L) {
+        store_slice(o + (int64_t)(start + my_q) * so.row + (int64_t)h * so.head + c0, ov, 1.0f / l);
+        if (c0 == 0) lse[(int64_t)(start + my_q) * heads + h] = m + logf(l);
+      }
     }
   }
   publish_header(src, iv, CAUSAL ? 1 : 0);
-  if (h == 0) publish_item(src, item, it);
+  if (h == 0 && part == 0 && L > 0) publish_item(src, item, it);
 }
 
 // dQ = scale * dS K with dS = P (dP - Delta), P = exp(S - LSE), dP = dO V^T;
@@ -2066,7 +2099,7 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
     float* __restrict__ delta, float* __restrict__ dq, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides so,
     Strides sdq, float scale, int total) {
-  constexpr int DPT = f32_dpt<D>(), TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
+  constexpr int DPT = 16, TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
   const ItemView iv = item_view<false>(src, tmax);
@@ -2075,19 +2108,26 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
     poison_stats(delta, total, heads);
     return;
   }
+  const int part = blockIdx.x % kF32Split;
   int item, h;
-  if (!map_block(heads, tmax, head_major, group, false, item, h) || item >= iv.count) return;
+  if (!map_block_at(blockIdx.x / kF32Split, heads, tmax, head_major, group, false, item, h) ||
+      item >= iv.count)
+    return;
   const int4 it = item_at<false>(src, iv, CAUSAL, item);
-  if (it.w == 0) return;
-  const int start = it.z, L = it.w, q0 = it.y * kBM;
+  const int start = it.z, L = it.w, q0 = it.y * kBM + part * kF32WgRows;
+  if (L == 0 || q0 >= L) return;
   const int hk = h / group;
   const int c0 = (threadIdx.x % TPR) * DPT;
   const float* kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
   const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
-  const int kend = CAUSAL ? min(L, q0 + kBM) : L;
-  for (int r0 = 0; r0 < kBM && q0 + r0 < L; r0 += RPP) {
+  const int kend = CAUSAL ? min(L, q0 + kF32WgRows) : L;
+  const float c = scale * kLog2e;
+  F32Stage<D, f32_threads<D>()> stage;
+  for (int r0 = 0; r0 < kF32WgRows && q0 + r0 < L; r0 += RPP) {
     const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
     const int64_t tok = start + min(my_q, L - 1);
+    const int kpass = CAUSAL ? min(kend, q0 + r0 + RPP) : kend;
+    stage.load(kh, sk.row, vh, sv.row, 0, kend);
     float qv[DPT], dov[DPT], dqv[DPT];
     float dl;
     {
@@ -2099,16 +2139,14 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
     }
     if (my_q < L && c0 == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
     const float lse2 = lse[tok * heads + h] * kLog2e;
-    const float c = scale * kLog2e;
 #pragma unroll
     for (int d = 0; d < DPT; ++d) dqv[d] = 0.f;
     const int qlim = CAUSAL ? min(my_q, L - 1) : L - 1;
-    const int kpass = CAUSAL ? min(kend, q0 + r0 + RPP) : kend;
     for (int kb = 0; kb < kpass; kb += KT) {
       __syncthreads();
-      stage_rows_f32<D>(sK, kh, sk.row, kb, kend);
-      stage_rows_f32<D>(sV, vh, sv.row, kb, kend);
+      stage.store(sK, sV);
       __syncthreads();
+      if (kb + KT < kpass) stage.load(kh, sk.row, vh, sv.row, kb + KT, kend);
       float dqt[DPT];
 #pragma unroll
       for (int d = 0; d < DPT; ++d) dqt[d] = 0.f;
@@ -2130,7 +2168,7 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
   }
 }
 
-// dV = P^T dO and dK = scale * dS^T Q for an item's 128 keys, summed over
+// dV = P^T dO and dK = scale * dS^T Q for 64 of an item's keys, summed over
 // the query heads that share their K/V head.
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dkv_f32_kernel(
@@ -2139,7 +2177,7 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dkv_f32_kernel(
     float* __restrict__ dk, float* __restrict__ dv, ItemSource src, int tmax, int head_major,
     int kv_heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk,
     Strides sdv, float scale, int total) {
-  constexpr int DPT = f32_dpt<D>(), TPR = f32_tpr<D>(), RPP = f32_rows<D>(), QT = kF32Rows;
+  constexpr int DPT = 16, TPR = f32_tpr<D>(), RPP = f32_rows<D>(), QT = kF32Rows;
   __shared__ __align__(16) float sQ[QT * D];
   __shared__ __align__(16) float sO[QT * D];  // dO rows
   __shared__ float sL[QT], sD[QT];             // LSE * log2(e) and Delta of those rows
@@ -2149,17 +2187,21 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dkv_f32_kernel(
     poison_rows(dv, sdv, total, kv_heads, D);
     return;
   }
+  const int part = blockIdx.x % kF32Split;
   int item, hk;
-  if (!map_block(kv_heads, tmax, head_major, 1, false, item, hk) || item >= iv.count) return;
+  if (!map_block_at(blockIdx.x / kF32Split, kv_heads, tmax, head_major, 1, false, item, hk) ||
+      item >= iv.count)
+    return;
   const int4 it = item_at<false>(src, iv, CAUSAL, item);
-  if (it.w == 0) return;
   const int start = it.z, L = it.w;
-  const int heads = kv_heads * group;
   const int nblk = (L + kBM - 1) / kBM;
-  const int k0 = (nblk - 1 - it.y) * kBM;  // key-major: the list's blk counts down
+  const int k0 = (nblk - 1 - it.y) * kBM + part * kF32WgRows;  // key-major: the list's blk counts down
+  if (L == 0 || k0 >= L) return;
+  const int heads = kv_heads * group;
   const int c0 = (threadIdx.x % TPR) * DPT;
   const float c = scale * kLog2e;
-  for (int r0 = 0; r0 < kBM && k0 + r0 < L; r0 += RPP) {
+  F32Stage<D, f32_threads<D>()> stage;
+  for (int r0 = 0; r0 < kF32WgRows && k0 + r0 < L; r0 += RPP) {
     const int my_k = k0 + r0 + (int)threadIdx.x / TPR;
     const int64_t tok = start + min(my_k, L - 1);
     float kv[DPT], vv[DPT], dkv[DPT], dvv[DPT];
@@ -2172,16 +2214,26 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dkv_f32_kernel(
       const int h = hk * group + gi;
       const float* qh = q + (int64_t)start * sq.row + (int64_t)h * sq.head;
       const float* dh = dout + (int64_t)start * sdo.row + (int64_t)h * sdo.head;
+      float pl = 0.f, pd = 0.f;  // the next tile's LSE and Delta (threads < QT)
+      auto load_rows = [&](int qb) {
+        const int qq = qb + (int)threadIdx.x;
+        pl = threadIdx.x < QT && qq < L ? lse[(int64_t)(start + qq) * heads + h] * kLog2e : 0.f;
+        pd = threadIdx.x < QT && qq < L ? delta[(int64_t)(start + qq) * heads + h] : 0.f;
+      };
+      stage.load(qh, sq.row, dh, sdo.row, qbeg, L);
+      load_rows(qbeg);
       for (int qb = qbeg; qb < L; qb += QT) {
         __syncthreads();
-        stage_rows_f32<D>(sQ, qh, sq.row, qb, L);
-        stage_rows_f32<D>(sO, dh, sdo.row, qb, L);
+        stage.store(sQ, sO);
         if (threadIdx.x < QT) {
-          const int qq = qb + (int)threadIdx.x;
-          sL[threadIdx.x] = qq < L ? lse[(int64_t)(start + qq) * heads + h] * kLog2e : 0.f;
-          sD[threadIdx.x] = qq < L ? delta[(int64_t)(start + qq) * heads + h] : 0.f;
+          sL[threadIdx.x] = pl;
+          sD[threadIdx.x] = pd;
         }
         __syncthreads();
+        if (qb + QT < L) {
+          stage.load(qh, sq.row, dh, sdo.row, qb + QT, L);
+          load_rows(qb + QT);
+        }
         float dkt[DPT], dvt[DPT];
 #pragma unroll
         for (int d = 0; d < DPT; ++d) dkt[d] = dvt[d] = 0.f;
@@ -2258,7 +2310,7 @@ int check_common(const char* fn, const int32_t* cu, int batch, int64_t total, in
   if (!workspace || workspace_bytes < need)
     return set_error(SCREE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
                      workspace ? workspace_bytes : (size_t)0);
-  if (tmax_for(batch, total) * heads > 0x7fffffffLL)
+  if (tmax_for(batch, total) * heads * (dtype == SCREE_DTYPE_F32 ? kF32Split : 1) > 0x7fffffffLL)
     return set_error(SCREE_ERR_INVALID, "%s: grid too large", fn);
   return SCREE_OK;
 }
@@ -2428,7 +2480,7 @@ template <int D, bool C>
 void launch_fwd_f32(const void* q, const void* k, const void* v, void* o, float* lse,
                     const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
                     float scale, int tmax, void* ws, int total, hipStream_t stream) {
-  const int64_t grid = (int64_t)tmax * heads;
+  const int64_t grid = (int64_t)tmax * heads * kF32Split;
   const int hm = attn_head_major(heads, tmax);
   hipLaunchKernelGGL((attn_fwd_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()), 0,
                      stream, static_cast<const float*>(q), static_cast<const float*>(k),
@@ -2444,7 +2496,7 @@ void launch_bwd_dq_f32(const void* dout, const void* q, const void* k, const voi
                        const void* o, const float* lse, void* dq, float* delta, int heads,
                        int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                        int total, hipStream_t stream) {
-  const int64_t grid = (int64_t)tmax * heads;
+  const int64_t grid = (int64_t)tmax * heads * kF32Split;
   const int hm = attn_head_major(heads, tmax);
   hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()),
                      0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
@@ -2462,7 +2514,7 @@ void launch_bwd_dkv_f32(const void* dout, const void* q, const void* k, const vo
                         const float* lse, const float* delta, void* dk, void* dv, int heads,
                         int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                         int total, hipStream_t stream) {
-  const int64_t grid = (int64_t)tmax * kv_heads;
+  const int64_t grid = (int64_t)tmax * kv_heads * kF32Split;
   const int hm = attn_head_major(kv_heads, tmax);
   hipLaunchKernelGGL((attn_bwd_dkv_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()),
                      0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
