@@ -26,7 +26,9 @@ RMSNorm / LayerNorm / fused add + RMSNorm forward and backward GB/s, varlen
 softmax forward and backward and packed <-> padded conversions GB/s at the
 config-2 shape, the reference's 27-shape sweep (head_dim x heads x mean
 length, fp16 causal, forward and forward+backward), torch's own SDPA on the same GPU for calibration (uniform
-lengths with cfg4's token count), the user-facing autograd step, config 1
+lengths with cfg4's token count), the vendor GEMM's fp16 rate on random and
+on constant operands (the clock this GPU holds on real data), the
+user-facing autograd step, config 1
 (the reference's CPU case) on the GPU path, and per-kernel HIP-event
 timings.  ``roofline`` describes the dominant kernel of the primary step;
 ``cpu_baseline`` times the numpy oracle (the reference's einsum call
@@ -345,6 +347,32 @@ def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup):
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def time_gemm_calibration(n=8192, reps=200):
+    """Calibration: the vendor GEMM (``torch.matmul``, ROCm's BLAS) on fp16
+    n x n by n x n, once with N(0,1) operands and once with all-ones operands.
+
+    The same instruction stream draws different power on different data: the
+    GPU holds its top clock on constant operands and lowers it on random
+    ones, so the random-operand rate is the dense matrix rate this GPU
+    sustains on real data, beside the published peak the roofline uses."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(11)
+    out = {}
+    for name, init in (("random", lambda: torch.randn(n, n, device=dev, dtype=torch.float16, generator=g)),
+                       ("ones", lambda: torch.ones(n, n, device=dev, dtype=torch.float16))):
+        a, b = init(), init()
+        c = torch.empty(n, n, device=dev, dtype=torch.float16)
+        fn = lambda: torch.matmul(a, b, out=c)  # noqa: E731
+        fn()
+        ms = _events_time(fn, reps)
+        tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac_of_published_peak": round(tf / PEAK_F16_TFLOPS, 4)}
+        del a, b, c
+    return out
+
+
 def time_config1_gpu(steps, warmup):
     """Config 1 (the reference's CPU plumbing case) on the GPU path.
 
@@ -653,6 +681,12 @@ def main() -> int:
             "ours_ms": round(ours["ms"], 4), "ours_tflops": round(ours["tflops"], 2),
             "torch_sdpa_ms": round(ref["ms"], 4), "torch_sdpa_tflops": round(ref["tflops"], 2)}
         log(f"calibration 16x760: ours {ours['tflops']:.0f} TF/s, torch SDPA {ref['tflops']:.0f} TF/s")
+        gm = time_gemm_calibration()
+        secondary["vendor_gemm_fp16_8192"] = {
+            "what": "torch.matmul fp16 8192x8192x8192, 200 back-to-back calls after the settle, "
+                    "N(0,1) operands vs all-ones operands (same kernels; the GPU lowers its "
+                    "clock on random data)", **gm}
+        log(f"vendor GEMM fp16 8192^3: random {gm['random']['tflops']:.0f} TF/s, ones {gm['ones']['tflops']:.0f} TF/s")
         if not args.no_sweep:
             secondary["reference_shape_sweep_fp16_causal"] = time_shape_sweep(20, 3)
         nr = time_norms(workloads.config2(), args.steps, args.warmup)
