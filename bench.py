@@ -27,7 +27,9 @@ softmax forward and backward and packed <-> padded conversions GB/s at the
 config-2 shape, the reference's 27-shape sweep (head_dim x heads x mean
 length, fp16 causal, forward and forward+backward), torch's own SDPA on the same GPU for calibration (uniform
 lengths with cfg4's token count), the vendor GEMM's fp16 rate on random and
-on constant operands (the clock this GPU holds on real data), the
+on constant operands (the clock this GPU holds on real data), config 4
+and config 5 run back to back for 3 s with the board's socket power and gfx
+clock sampled by ``amd-smi`` (the rate at the board power limit), the
 user-facing autograd step, config 1
 (the reference's CPU case) on the GPU path, and per-kernel HIP-event
 timings.  ``roofline`` describes the dominant kernel of the primary step;
@@ -347,6 +349,65 @@ def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup):
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def _read_power():
+    """(socket power W, gfx clock MHz) of GPU 0 from ``amd-smi`` run as a child
+    process, or None where the tool or the fields are missing."""
+    import re
+    import subprocess
+
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-p", "-c"], capture_output=True, text=True, timeout=10)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    pw = re.search(r"SOCKET_POWER:\s*(\d+(?:\.\d+)?)\s*W", r.stdout)
+    ck = re.search(r"GFX_0:\s*\n\s*CLK:\s*(\d+)\s*MHz", r.stdout)
+    if not pw or not ck:
+        return None
+    return float(pw.group(1)), float(ck.group(1))
+
+
+def time_sustained(fn, steps_per_call, seconds=3.0):
+    """Milliseconds per step of ``fn`` (``steps_per_call`` steps per call)
+    launched back to back for ``seconds``, with the board's socket power and
+    the gfx clock sampled beside it (medians over the samples after the first
+    half second).  Short timed regions run at a higher clock than this: the
+    GPU's power management lets the clock down over the first seconds of
+    load, to hold the board power limit."""
+    import threading
+
+    import torch
+
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            s = _read_power()
+            if s is None:
+                return
+            samples.append((time.perf_counter(), *s))
+
+    fn()
+    torch.cuda.synchronize()
+    th = threading.Thread(target=sampler, daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+        n += 4
+    dt = time.perf_counter() - t0
+    stop.set()
+    th.join(timeout=15)
+    late = [s for s in samples if s[0] - t0 > 0.5]
+    return {"seconds": round(dt, 2), "steps": n * steps_per_call,
+            "ms_per_step": round(dt * 1e3 / (n * steps_per_call), 4),
+            "socket_power_W": statistics.median(s[1] for s in late) if late else None,
+            "gfx_clock_MHz": statistics.median(s[2] for s in late) if late else None,
+            "power_samples": len(late)}
+
+
 def time_gemm_calibration(n=8192, reps=200):
     """Calibration: the vendor GEMM (``torch.matmul``, ROCm's BLAS) on fp16
     n x n by n x n, once with N(0,1) operands and once with all-ones operands.
@@ -611,7 +672,7 @@ def main() -> int:
 
     cfg4 = workloads.config4()
     log(f"primary: {cfg4.name} lengths={cfg4.lengths}")
-    prim, _ = time_attention(cfg4, fp16, args.steps, args.warmup, backward=True, per_kernel=True)
+    prim, case4 = time_attention(cfg4, fp16, args.steps, args.warmup, backward=True, per_kernel=True)
     log(f"primary: {prim['ms']:.4f} ms/step, {prim['tflops']:.1f} TFLOP/s "
         f"(one-step graphs: {prim['graph1_ms']:.4f}, eager launches: {prim['eager_ms']:.4f} ms/step)")
 
@@ -641,6 +702,13 @@ def main() -> int:
                                           "tflops": round(cfg4.fwd_flops() * 3.5 / (prim["graph1_ms"] * 1e-3)
                                                           / 1e12, 2)}}
     if not args.primary_only:
+        g4 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g4):
+            for _ in range(10):
+                case4.step_fwd_bwd()
+        secondary["cfg4_sustained_3s"] = time_sustained(g4.replay, 10)
+        log(f"cfg4 sustained: {secondary['cfg4_sustained_3s']}")
+        del g4
         small = max(3, args.steps // 2)
         cfg3 = workloads.config3()
         r, _ = time_attention(cfg3, fp16, args.steps, args.warmup, backward=False, per_kernel=True)
@@ -659,10 +727,12 @@ def main() -> int:
         secondary["cfg1_gpu"] = time_config1_gpu(args.steps, args.warmup)
         log(f"cfg1 on the GPU: {secondary['cfg1_gpu']}")
         cfg5 = workloads.config5()
-        r, _ = time_attention(cfg5, torch.bfloat16, small, 2, backward=True, per_kernel=True)
+        r, case5 = time_attention(cfg5, torch.bfloat16, small, 2, backward=True, per_kernel=True)
         secondary["cfg5_fwd_bwd_bf16"] = {"ms": round(r["ms"], 3), "tflops": round(r["tflops"], 2),
                                           "mfma_frac": round(r["mfma_frac"], 4),
-                                          "kernels_us": {k: round(v * 1e3, 1) for k, v in r["kernels_ms"].items()}}
+                                          "kernels_us": {k: round(v * 1e3, 1) for k, v in r["kernels_ms"].items()},
+                                          "sustained_3s": time_sustained(case5.step_fwd_bwd, 1)}
+        del case5
         log(f"cfg5: {r['ms']:.3f} ms {r['tflops']:.1f} TFLOP/s")
         gq = workloads.config4()
         gq.name = "cfg4_gqa_16q_4kv"
