@@ -554,8 +554,10 @@ __global__ __launch_bounds__(1024) void attn_big_schedule_kernel(
 
 // ------------------------------------------------------- tile staging
 // Raw buffer resource for `bytes` bytes at `base` (gfx9 descriptor: stride 0,
-// dword3 = 0x00020000).  Loads at offsets past `bytes` return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+// dword3 = 0x00020000).  Loads at offsets past `bytes` return zeros.  (Used
+// only in device passes, hence maybe_unused for the host pass.)
+[[maybe_unused]] __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                                             uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
