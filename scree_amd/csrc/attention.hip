@@ -1898,8 +1898,9 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
 // (its torch branch, reference/varlen_attention.py:90-113).  The matrix
 // instructions run fp32 at a sixteenth of their 16-bit rate, so these kernels
 // use FP32 FMAs instead: each row of an item (a query, or a key for dK/dV) is
-// split over TPR = D / 16 consecutive lanes holding 16 columns each, a dot
-// product is 16 FMAs plus a DPP sum over those lanes, and K / V (or Q / dO)
+// split over TPR consecutive lanes holding DPT columns each (DPT = 16, or 4-8
+// for small launches, below), a dot product is DPT FMAs plus a DPP sum over
+// those lanes, and K / V (or Q / dO)
 // rows are staged 32 at a time in LDS, where every row group of a wave reads
 // the same staged row (a broadcast); the next 32 rows are loaded into
 // registers while the current ones are used.  Two workgroups share an item,
@@ -1915,17 +1916,32 @@ __global__ __launch_bounds__(kThreads, (dkv_waves<D, CAUSAL>())) void attn_bwd_d
 constexpr int kF32Split = 2;                // workgroups per item
 constexpr int kF32WgRows = kBM / kF32Split;  // rows of an item per workgroup
 constexpr int kF32Rows = 32;                // keys (forward, dQ) or queries (dK/dV) per LDS tile
+// Columns per lane: 16 (the narrow form), or, for launches too small to
+// give every SIMD a wave in that form, max(4, D / 16) (the wide form: 4 to
+// 16 lanes per row, so each row's chain of keys is 2-4x shorter and a
+// workgroup holds up to 4x the waves, at the price of repeating each row's
+// softmax arithmetic on more lanes).  Both keep every row within 16 lanes.
+// Measured (MI355X, causal): config 1's 1,980 tokens x 4 heads x 32, a
+// narrow grid of 512 waves, run 56 -> 34 us forward and 182 -> 117 us
+// forward + backward in the wide form; 7,168 tokens x 8 heads x 64 (3,776
+// narrow waves) ran 13 % (forward) and 41 % (forward + backward) slower in
+// it, so only launches below one narrow wave per SIMD take it.
+constexpr int kF32NarrowDpt = 16;
 template <int D>
+constexpr int f32_wide_dpt() {
+  return D / 16 > 4 ? D / 16 : 4;
+}
+template <int D, int DPT>
 constexpr int f32_tpr() {
-  return D / 16;  // lanes per row, 16 columns each
+  return D / DPT;  // lanes per row
 }
-template <int D>
+template <int D, int DPT>
 constexpr int f32_rows() {
-  return kF32WgRows * f32_tpr<D>() <= 512 ? kF32WgRows : 512 / f32_tpr<D>();  // rows per pass
+  return kF32WgRows * f32_tpr<D, DPT>() <= 512 ? kF32WgRows : 512 / f32_tpr<D, DPT>();  // rows per pass
 }
-template <int D>
+template <int D, int DPT>
 constexpr int f32_threads() {
-  return f32_rows<D>() * f32_tpr<D>();
+  return f32_rows<D, DPT>() * f32_tpr<D, DPT>();
 }
 
 // Sum over the TPR (1 to 16) consecutive lanes of one row, by the DPP steps
@@ -2006,12 +2022,12 @@ struct F32Stage {
   }
 };
 
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(f32_threads<D>()) void attn_fwd_f32_kernel(
+template <int D, bool CAUSAL, int DPT>
+__global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_fwd_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ lse, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sq, Strides sk, Strides sv, Strides so, float scale, int total) {
-  constexpr int DPT = 16, TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), KT = kF32Rows;
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
   const ItemView iv = item_view<true>(src, tmax);
@@ -2036,7 +2052,7 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_fwd_f32_kernel(
     const float* kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
     const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
     const int kend = CAUSAL ? min(L, q0 + kF32WgRows) : L;
-    F32Stage<D, f32_threads<D>()> stage;
+    F32Stage<D, f32_threads<D, DPT>()> stage;
     for (int r0 = 0; r0 < kF32WgRows && q0 + r0 < L; r0 += RPP) {
       const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
       // rows past L compute on row L-1 and store nothing
@@ -2094,14 +2110,14 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_fwd_f32_kernel(
 
 // dQ = scale * dS K with dS = P (dP - Delta), P = exp(S - LSE), dP = dO V^T;
 // Delta = rowsum(O * dO) is formed here and written out for the dK/dV pass.
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
+template <int D, bool CAUSAL, int DPT>
+__global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dq_f32_kernel(
     const float* __restrict__ dout, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ o, const float* __restrict__ lse,
     float* __restrict__ delta, float* __restrict__ dq, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides so,
     Strides sdq, float scale, int total) {
-  constexpr int DPT = 16, TPR = f32_tpr<D>(), RPP = f32_rows<D>(), KT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), KT = kF32Rows;
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
   const ItemView iv = item_view<false>(src, tmax);
@@ -2124,7 +2140,7 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
   const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
   const int kend = CAUSAL ? min(L, q0 + kF32WgRows) : L;
   const float c = scale * kLog2e;
-  F32Stage<D, f32_threads<D>()> stage;
+  F32Stage<D, f32_threads<D, DPT>()> stage;
   for (int r0 = 0; r0 < kF32WgRows && q0 + r0 < L; r0 += RPP) {
     const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
     const int64_t tok = start + min(my_q, L - 1);
@@ -2172,14 +2188,14 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dq_f32_kernel(
 
 // dV = P^T dO and dK = scale * dS^T Q for 64 of an item's keys, summed over
 // the query heads that share their K/V head.
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dkv_f32_kernel(
+template <int D, bool CAUSAL, int DPT>
+__global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dkv_f32_kernel(
     const float* __restrict__ dout, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dk, float* __restrict__ dv, ItemSource src, int tmax, int head_major,
     int kv_heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk,
     Strides sdv, float scale, int total) {
-  constexpr int DPT = 16, TPR = f32_tpr<D>(), RPP = f32_rows<D>(), QT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), QT = kF32Rows;
   __shared__ __align__(16) float sQ[QT * D];
   __shared__ __align__(16) float sO[QT * D];  // dO rows
   __shared__ float sL[QT], sD[QT];             // LSE * log2(e) and Delta of those rows
@@ -2202,7 +2218,7 @@ __global__ __launch_bounds__(f32_threads<D>()) void attn_bwd_dkv_f32_kernel(
   const int heads = kv_heads * group;
   const int c0 = (threadIdx.x % TPR) * DPT;
   const float c = scale * kLog2e;
-  F32Stage<D, f32_threads<D>()> stage;
+  F32Stage<D, f32_threads<D, DPT>()> stage;
   for (int r0 = 0; r0 < kF32WgRows && k0 + r0 < L; r0 += RPP) {
     const int my_k = k0 + r0 + (int)threadIdx.x / TPR;
     const int64_t tok = start + min(my_k, L - 1);
@@ -2478,13 +2494,22 @@ void launch_bwd_dkv_t(const void* dout, const void* q, const void* k, const void
     else { if (causal) FN<256, true>(__VA_ARGS__); else FN<256, false>(__VA_ARGS__); }           \
   } while (0)
 
-template <int D, bool C>
-void launch_fwd_f32(const void* q, const void* k, const void* v, void* o, float* lse,
-                    const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
-                    float scale, int tmax, void* ws, int total, hipStream_t stream) {
+// The fp32 form for a grid: wide when the narrow form would give the GPU's
+// 1,024 SIMDs less than a wave each.
+template <int D>
+bool f32_use_wide(int64_t grid) {
+  constexpr int64_t waves = (f32_threads<D, kF32NarrowDpt>() + kWave - 1) / kWave;
+  return f32_wide_dpt<D>() != kF32NarrowDpt && grid * waves < 1024;
+}
+
+template <int D, bool C, int DPT>
+void launch_fwd_f32_as(const void* q, const void* k, const void* v, void* o, float* lse,
+                       const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
+                       float scale, int tmax, void* ws, int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads * kF32Split;
   const int hm = attn_head_major(heads, tmax);
-  hipLaunchKernelGGL((attn_fwd_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()), 0,
+  hipLaunchKernelGGL((attn_fwd_f32_kernel<D, C, DPT>), dim3((unsigned)grid),
+                     dim3(f32_threads<D, DPT>()), 0,
                      stream, static_cast<const float*>(q), static_cast<const float*>(k),
                      static_cast<const float*>(v), static_cast<float*>(o), lse,
                      fwd_item_source(ws, cu, batch, total, tmax, heads, D, hm), tmax, hm, heads,
@@ -2492,16 +2517,28 @@ void launch_fwd_f32(const void* q, const void* k, const void* v, void* o, float*
                      Strides{st[4], st[5]}, Strides{st[6], st[7]}, scale, total);
 }
 
-// strides: {dout, q, k, v, o, dq} x {row, head}
 template <int D, bool C>
-void launch_bwd_dq_f32(const void* dout, const void* q, const void* k, const void* v,
-                       const void* o, const float* lse, void* dq, float* delta, int heads,
-                       int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
-                       int total, hipStream_t stream) {
+void launch_fwd_f32(const void* q, const void* k, const void* v, void* o, float* lse,
+                    const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
+                    float scale, int tmax, void* ws, int total, hipStream_t stream) {
+  if (f32_use_wide<D>((int64_t)tmax * heads * kF32Split))
+    launch_fwd_f32_as<D, C, f32_wide_dpt<D>()>(q, k, v, o, lse, cu, batch, heads, kv_heads, st,
+                                               scale, tmax, ws, total, stream);
+  else
+    launch_fwd_f32_as<D, C, kF32NarrowDpt>(q, k, v, o, lse, cu, batch, heads, kv_heads, st, scale,
+                                           tmax, ws, total, stream);
+}
+
+// strides: {dout, q, k, v, o, dq} x {row, head}
+template <int D, bool C, int DPT>
+void launch_bwd_dq_f32_as(const void* dout, const void* q, const void* k, const void* v,
+                          const void* o, const float* lse, void* dq, float* delta, int heads,
+                          int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
+                          int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads * kF32Split;
   const int hm = attn_head_major(heads, tmax);
-  hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()),
-                     0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
+  hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, C, DPT>), dim3((unsigned)grid),
+                     dim3(f32_threads<D, DPT>()), 0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
                      static_cast<const float*>(k), static_cast<const float*>(v),
                      static_cast<const float*>(o), lse, delta, static_cast<float*>(dq),
                      list_item_source(ws, total, tmax, hm), tmax, hm, heads, heads / kv_heads,
@@ -2510,22 +2547,48 @@ void launch_bwd_dq_f32(const void* dout, const void* q, const void* k, const voi
                      total);
 }
 
-// strides: {dout, q, k, v, dk, dv} x {row, head}; one workgroup per (item, K/V head)
 template <int D, bool C>
-void launch_bwd_dkv_f32(const void* dout, const void* q, const void* k, const void* v,
-                        const float* lse, const float* delta, void* dk, void* dv, int heads,
-                        int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
-                        int total, hipStream_t stream) {
+void launch_bwd_dq_f32(const void* dout, const void* q, const void* k, const void* v,
+                       const void* o, const float* lse, void* dq, float* delta, int heads,
+                       int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
+                       int total, hipStream_t stream) {
+  if (f32_use_wide<D>((int64_t)tmax * heads * kF32Split))
+    launch_bwd_dq_f32_as<D, C, f32_wide_dpt<D>()>(dout, q, k, v, o, lse, dq, delta, heads, kv_heads,
+                                                  st, scale, tmax, ws, total, stream);
+  else
+    launch_bwd_dq_f32_as<D, C, kF32NarrowDpt>(dout, q, k, v, o, lse, dq, delta, heads, kv_heads, st,
+                                              scale, tmax, ws, total, stream);
+}
+
+// strides: {dout, q, k, v, dk, dv} x {row, head}; one workgroup per (item, K/V head)
+template <int D, bool C, int DPT>
+void launch_bwd_dkv_f32_as(const void* dout, const void* q, const void* k, const void* v,
+                           const float* lse, const float* delta, void* dk, void* dv, int heads,
+                           int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
+                           int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * kv_heads * kF32Split;
   const int hm = attn_head_major(kv_heads, tmax);
-  hipLaunchKernelGGL((attn_bwd_dkv_f32_kernel<D, C>), dim3((unsigned)grid), dim3(f32_threads<D>()),
-                     0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
+  hipLaunchKernelGGL((attn_bwd_dkv_f32_kernel<D, C, DPT>), dim3((unsigned)grid),
+                     dim3(f32_threads<D, DPT>()), 0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
                      static_cast<const float*>(k), static_cast<const float*>(v), lse, delta,
                      static_cast<float*>(dk), static_cast<float*>(dv),
                      list_item_source(ws, total, tmax, hm), tmax, hm, kv_heads,
                      heads / kv_heads, Strides{st[0], st[1]}, Strides{st[2], st[3]},
                      Strides{st[4], st[5]}, Strides{st[6], st[7]}, Strides{st[8], st[9]},
                      Strides{st[10], st[11]}, scale, total);
+}
+
+template <int D, bool C>
+void launch_bwd_dkv_f32(const void* dout, const void* q, const void* k, const void* v,
+                        const float* lse, const float* delta, void* dk, void* dv, int heads,
+                        int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
+                        int total, hipStream_t stream) {
+  if (f32_use_wide<D>((int64_t)tmax * kv_heads * kF32Split))
+    launch_bwd_dkv_f32_as<D, C, f32_wide_dpt<D>()>(dout, q, k, v, lse, delta, dk, dv, heads,
+                                                   kv_heads, st, scale, tmax, ws, total, stream);
+  else
+    launch_bwd_dkv_f32_as<D, C, kF32NarrowDpt>(dout, q, k, v, lse, delta, dk, dv, heads, kv_heads,
+                                               st, scale, tmax, ws, total, stream);
 }
 
 }  // namespace

@@ -98,6 +98,38 @@ def test_fp32_past_64_sequences():
     run_fp32_case(lengths, 2, 64, True, seed=600)
 
 
+def f32_form(lengths, heads, dim):
+    """The column layout an fp32 launch takes: "narrow" (16 columns per lane)
+    unless that form would give the 1,024 SIMDs less than a wave each and
+    head_dim is below 256 ("wide": max(4, dim / 16) columns per lane).
+    Restates the launchers' choice so each test knows which form it checks."""
+    tmax = -(-sum(lengths) // 128) + len(lengths)
+    tpr = dim // 16
+    rows = 64 if 64 * tpr <= 512 else 512 // tpr
+    waves = -(-(rows * tpr) // 64)
+    if max(4, dim // 16) == 16:
+        return "narrow"
+    return "wide" if tmax * heads * 2 * waves < 1024 else "narrow"
+
+
+@pytest.mark.parametrize("dim,heads", [(16, 72), (32, 40), (64, 20), (128, 10)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fp32_narrow_form(dim, heads, causal):
+    """Launches large enough for the narrow form (the other tests here are
+    small enough for the wide one)."""
+    lengths = [200, 129, 64, 300, 17, 1, 90, 255, 128, 40, 77, 150, 33, 96, 5, 250]
+    assert f32_form(lengths, heads, dim) == "narrow"
+    run_fp32_case(lengths, heads, dim, causal, seed=800 + dim, kv_heads=heads // 2)
+
+
+def test_fp32_forms_of_the_other_tests():
+    """Both forms are covered at every head_dim below 256."""
+    for dim in (16, 32, 64, 128):
+        assert f32_form(EDGE_LENGTHS, 2, dim) == "wide"
+    assert f32_form(EDGE_LENGTHS, 8, 128) == "narrow"  # the grouped-query case
+    assert f32_form(EDGE_LENGTHS, 2, 256) == "narrow"
+
+
 def test_fp32_run_to_run_identical():
     import scree_amd
     from scree_amd.kernels import varlen_attention
