@@ -1,4 +1,5 @@
-"""HIP-graph capture of one attention step (scheduler, forward, dQ, dK/dV).
+"""HIP-graph capture of one attention step (scheduler, forward, dQ, dK/dV),
+in fp16, bf16 and fp32 (the FP32-FMA kernels).
 
 Callers (and bench.py) may capture the launches in a graph: the kernels
 allocate nothing and the library issues no memset.  Every replay must give
@@ -48,13 +49,15 @@ def _case(lengths, heads, kv_heads, dim, dtype, causal, split=False):
 OUTS = ("out", "lse", "delta", "dq", "dk", "dv")
 
 
-@pytest.mark.parametrize("kv_heads,split", [(8, False), (2, False), (2, True)])
-def test_graph_replays_match_eager(kv_heads, split):
+@pytest.mark.parametrize("kv_heads,split,dtype", [
+    (8, False, torch.float16), (2, False, torch.float16), (2, True, torch.float16),
+    (8, False, torch.bfloat16), (2, False, torch.float32)])
+def test_graph_replays_match_eager(kv_heads, split, dtype):
     from scree_amd.kernels.hip import attention as A
 
     lengths = [300, 17, 129, 640, 1]
-    say(f"case: graph replay lengths={lengths} H=8 Hkv={kv_heads} D=64 fp16 causal split={split}")
-    t, step = _case(lengths, 8, kv_heads, 64, torch.float16, True, split)
+    say(f"case: graph replay lengths={lengths} H=8 Hkv={kv_heads} D=64 {dtype} causal split={split}")
+    t, step = _case(lengths, 8, kv_heads, 64, dtype, True, split)
     if split:
         assert t["ws"].numel() > A.workspace_bytes(len(lengths), sum(lengths), 64)
     step()
@@ -73,7 +76,7 @@ def test_graph_replays_match_eager(kv_heads, split):
         for k in OUTS:
             assert torch.equal(t[k], want[k]), f"replay {rep}: {k} differs from the eager step"
     # new inputs copied into the captured buffers: the replay follows them
-    t["q"].copy_(randn(tuple(t["q"].shape), torch.float16, 99))
+    t["q"].copy_(randn(tuple(t["q"].shape), dtype, 99))
     step()
     torch.cuda.synchronize()
     want = {k: t[k].clone() for k in OUTS}
