@@ -1935,13 +1935,17 @@ template <int D, int DPT>
 constexpr int f32_tpr() {
   return D / DPT;  // lanes per row
 }
-template <int D, int DPT>
-constexpr int f32_rows() {
-  return kF32WgRows * f32_tpr<D, DPT>() <= 512 ? kF32WgRows : 512 / f32_tpr<D, DPT>();  // rows per pass
+// KG key groups per row (forward, wide form): the row's keys are dealt out
+// to KG groups of TPR lanes, each keeping its own softmax state, merged at
+// the end of the row pass.
+template <int D, int DPT, int KG = 1>
+constexpr int f32_rows() {  // rows per pass
+  return kF32WgRows * f32_tpr<D, DPT>() * KG <= 512 * KG ? kF32WgRows
+                                                         : 512 * KG / (f32_tpr<D, DPT>() * KG);
 }
-template <int D, int DPT>
+template <int D, int DPT, int KG = 1>
 constexpr int f32_threads() {
-  return f32_rows<D, DPT>() * f32_tpr<D, DPT>();
+  return f32_rows<D, DPT, KG>() * f32_tpr<D, DPT>() * KG;
 }
 
 // Sum over the TPR (1 to 16) consecutive lanes of one row, by the DPP steps
@@ -2022,12 +2026,13 @@ struct F32Stage {
   }
 };
 
-template <int D, bool CAUSAL, int DPT>
-__global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_fwd_f32_kernel(
+template <int D, bool CAUSAL, int DPT, int KG>
+__global__ __launch_bounds__((f32_threads<D, DPT, KG>())) void attn_fwd_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ lse, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sq, Strides sk, Strides sv, Strides so, float scale, int total) {
-  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), KT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT, KG>(), KT = kF32Rows;
+  static_assert(KT % KG == 0 && (KG == 1 || KG == 2), "one or two key groups");
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
   const ItemView iv = item_view<true>(src, tmax);
@@ -2052,9 +2057,10 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_fwd_f32_kernel(
     const float* kh = k + (int64_t)start * sk.row + (int64_t)hk * sk.head;
     const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
     const int kend = CAUSAL ? min(L, q0 + kF32WgRows) : L;
-    F32Stage<D, f32_threads<D, DPT>()> stage;
+    const int kg = KG > 1 ? ((int)threadIdx.x / TPR) % KG : 0;  // this lane's key group
+    F32Stage<D, f32_threads<D, DPT, KG>()> stage;
     for (int r0 = 0; r0 < kF32WgRows && q0 + r0 < L; r0 += RPP) {
-      const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
+      const int my_q = q0 + r0 + (int)threadIdx.x / (TPR * KG);
       // rows past L compute on row L-1 and store nothing
       float qv[DPT], ov[DPT];
       load_slice(qv, q + (int64_t)(start + min(my_q, L - 1)) * sq.row + (int64_t)h * sq.head + c0);
@@ -2069,27 +2075,31 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_fwd_f32_kernel(
         stage.store(sK, sV);
         __syncthreads();
         if (kb + KT < kpass) stage.load(kh, sk.row, vh, sv.row, kb + KT, kend);
-        float s[KT];
+        float s[KT / KG];  // this group's keys of the tile: kg, kg + KG, ...
         float tile_m = kNegInf;
 #pragma unroll
-        for (int i = 0; i < KT; ++i) {
+        for (int j = 0; j < KT / KG; ++j) {
+          const int i = j * KG + kg;
           float kr[DPT];
           load_slice(kr, sK + i * D + c0);
           const float dotv = row_sum<TPR>(dot_slice(qv, kr)) * scale;
-          s[i] = kb + i <= qlim ? dotv : kNegInf;
-          tile_m = fmaxf(tile_m, s[i]);
+          s[j] = kb + i <= qlim ? dotv : kNegInf;
+          tile_m = fmaxf(tile_m, s[j]);
         }
-        // key 0 is in every row's first tile, so m is finite from then on
+        // key 0 is in every row's first tile, so m is finite from then on;
+        // with two key groups the second may see no key of a row at all
+        // (row 0, or a length-1 sequence): its m stays -inf, its weights 0
         const float m_new = fmaxf(m, tile_m);
-        const float alpha = fast_exp2((m - m_new) * kLog2e);
+        const float m_ref = KG > 1 && m_new == kNegInf ? 0.f : m_new;
+        const float alpha = fast_exp2((m - m_ref) * kLog2e);
         float ot[DPT], lt = 0.f;
 #pragma unroll
         for (int d = 0; d < DPT; ++d) ot[d] = 0.f;
 #pragma unroll 4
-        for (int i = 0; i < KT; ++i) {
-          const float p = fast_exp2((s[i] - m_new) * kLog2e);
+        for (int j = 0; j < KT / KG; ++j) {
+          const float p = fast_exp2((s[j] - m_ref) * kLog2e);
           float vr[DPT];
-          load_slice(vr, sV + i * D + c0);
+          load_slice(vr, sV + (j * KG + kg) * D + c0);
           lt += p;
           axpy_slice(ot, p, vr);
         }
@@ -2098,7 +2108,19 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_fwd_f32_kernel(
         for (int d = 0; d < DPT; ++d) ov[d] = fmaf(ov[d], alpha, ot[d]);
         m = m_new;
       }
-      if (my_q < L) {
+      if constexpr (KG > 1) {  // merge the two groups' states (lanes TPR apart)
+        const float m_all = fmaxf(m, __shfl_xor(m, TPR, kWave));  // group 0 holds key 0: finite
+        const float a = fast_exp2((m - m_all) * kLog2e);
+        l *= a;
+        l += __shfl_xor(l, TPR, kWave);
+#pragma unroll
+        for (int d = 0; d < DPT; ++d) {
+          ov[d] *= a;
+          ov[d] += __shfl_xor(ov[d], TPR, kWave);
+        }
+        m = m_all;
+      }
+      if (my_q < L && kg == 0) {
         store_slice(o + (int64_t)(start + my_q) * so.row + (int64_t)h * so.head + c0, ov, 1.0f / l);
         if (c0 == 0) lse[(int64_t)(start + my_q) * heads + h] = m + logf(l);
       }
@@ -2110,14 +2132,15 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_fwd_f32_kernel(
 
 // dQ = scale * dS K with dS = P (dP - Delta), P = exp(S - LSE), dP = dO V^T;
 // Delta = rowsum(O * dO) is formed here and written out for the dK/dV pass.
-template <int D, bool CAUSAL, int DPT>
-__global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dq_f32_kernel(
+template <int D, bool CAUSAL, int DPT, int KG>
+__global__ __launch_bounds__((f32_threads<D, DPT, KG>())) void attn_bwd_dq_f32_kernel(
     const float* __restrict__ dout, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ o, const float* __restrict__ lse,
     float* __restrict__ delta, float* __restrict__ dq, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides so,
     Strides sdq, float scale, int total) {
-  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), KT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT, KG>(), KT = kF32Rows;
+  static_assert(KT % KG == 0 && (KG == 1 || KG == 2), "one or two key groups");
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
   const ItemView iv = item_view<false>(src, tmax);
@@ -2140,9 +2163,10 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dq_f32_kerne
   const float* vh = v + (int64_t)start * sv.row + (int64_t)hk * sv.head;
   const int kend = CAUSAL ? min(L, q0 + kF32WgRows) : L;
   const float c = scale * kLog2e;
-  F32Stage<D, f32_threads<D, DPT>()> stage;
+  const int kg = KG > 1 ? ((int)threadIdx.x / TPR) % KG : 0;  // this lane's key group
+  F32Stage<D, f32_threads<D, DPT, KG>()> stage;
   for (int r0 = 0; r0 < kF32WgRows && q0 + r0 < L; r0 += RPP) {
-    const int my_q = q0 + r0 + (int)threadIdx.x / TPR;
+    const int my_q = q0 + r0 + (int)threadIdx.x / (TPR * KG);
     const int64_t tok = start + min(my_q, L - 1);
     const int kpass = CAUSAL ? min(kend, q0 + r0 + RPP) : kend;
     stage.load(kh, sk.row, vh, sv.row, 0, kend);
@@ -2155,7 +2179,7 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dq_f32_kerne
       load_slice(ov, o + tok * so.row + (int64_t)h * so.head + c0);
       dl = row_sum<TPR>(dot_slice(ov, dov));
     }
-    if (my_q < L && c0 == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
+    if (my_q < L && c0 == 0 && kg == 0) delta[(int64_t)(start + my_q) * heads + h] = dl;
     const float lse2 = lse[tok * heads + h] * kLog2e;
 #pragma unroll
     for (int d = 0; d < DPT; ++d) dqv[d] = 0.f;
@@ -2169,7 +2193,8 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dq_f32_kerne
 #pragma unroll
       for (int d = 0; d < DPT; ++d) dqt[d] = 0.f;
 #pragma unroll 2
-      for (int i = 0; i < KT; ++i) {
+      for (int j = 0; j < KT / KG; ++j) {  // this group's keys: kg, kg + KG, ...
+        const int i = j * KG + kg;
         float kr[DPT], vr[DPT];
         load_slice(kr, sK + i * D + c0);
         load_slice(vr, sV + i * D + c0);
@@ -2181,21 +2206,26 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dq_f32_kerne
 #pragma unroll
       for (int d = 0; d < DPT; ++d) dqv[d] += dqt[d];
     }
-    if (my_q < L)
+    if constexpr (KG > 1) {  // the two groups' sums (lanes TPR apart)
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) dqv[d] += __shfl_xor(dqv[d], TPR, kWave);
+    }
+    if (my_q < L && kg == 0)
       store_slice(dq + (int64_t)(start + my_q) * sdq.row + (int64_t)h * sdq.head + c0, dqv, scale);
   }
 }
 
 // dV = P^T dO and dK = scale * dS^T Q for 64 of an item's keys, summed over
 // the query heads that share their K/V head.
-template <int D, bool CAUSAL, int DPT>
-__global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dkv_f32_kernel(
+template <int D, bool CAUSAL, int DPT, int KG>
+__global__ __launch_bounds__((f32_threads<D, DPT, KG>())) void attn_bwd_dkv_f32_kernel(
     const float* __restrict__ dout, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dk, float* __restrict__ dv, ItemSource src, int tmax, int head_major,
     int kv_heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk,
     Strides sdv, float scale, int total) {
-  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), QT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT, KG>(), QT = kF32Rows;
+  static_assert(QT % KG == 0 && (KG == 1 || KG == 2), "one or two query groups");
   __shared__ __align__(16) float sQ[QT * D];
   __shared__ __align__(16) float sO[QT * D];  // dO rows
   __shared__ float sL[QT], sD[QT];             // LSE * log2(e) and Delta of those rows
@@ -2218,9 +2248,10 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dkv_f32_kern
   const int heads = kv_heads * group;
   const int c0 = (threadIdx.x % TPR) * DPT;
   const float c = scale * kLog2e;
-  F32Stage<D, f32_threads<D, DPT>()> stage;
+  const int kg = KG > 1 ? ((int)threadIdx.x / TPR) % KG : 0;  // this lane's query group
+  F32Stage<D, f32_threads<D, DPT, KG>()> stage;
   for (int r0 = 0; r0 < kF32WgRows && k0 + r0 < L; r0 += RPP) {
-    const int my_k = k0 + r0 + (int)threadIdx.x / TPR;
+    const int my_k = k0 + r0 + (int)threadIdx.x / (TPR * KG);
     const int64_t tok = start + min(my_k, L - 1);
     float kv[DPT], vv[DPT], dkv[DPT], dvv[DPT];
     load_slice(kv, k + tok * sk.row + (int64_t)hk * sk.head + c0);
@@ -2256,7 +2287,8 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dkv_f32_kern
 #pragma unroll
         for (int d = 0; d < DPT; ++d) dkt[d] = dvt[d] = 0.f;
 #pragma unroll 2
-        for (int i = 0; i < QT; ++i) {
+        for (int j = 0; j < QT / KG; ++j) {  // this group's queries: kg, kg + KG, ...
+          const int i = j * KG + kg;
           const int qq = qb + i;
           float qr[DPT], orow[DPT];
           load_slice(qr, sQ + i * D + c0);
@@ -2275,7 +2307,14 @@ __global__ __launch_bounds__((f32_threads<D, DPT>())) void attn_bwd_dkv_f32_kern
         }
       }
     }
-    if (my_k < L) {
+    if constexpr (KG > 1) {  // the two groups' sums (lanes TPR apart)
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) {
+        dkv[d] += __shfl_xor(dkv[d], TPR, kWave);
+        dvv[d] += __shfl_xor(dvv[d], TPR, kWave);
+      }
+    }
+    if (my_k < L && kg == 0) {
       store_slice(dk + (int64_t)(start + my_k) * sdk.row + (int64_t)hk * sdk.head + c0, dkv, scale);
       store_slice(dv + (int64_t)(start + my_k) * sdv.row + (int64_t)hk * sdv.head + c0, dvv, 1.0f);
     }
@@ -2502,14 +2541,14 @@ bool f32_use_wide(int64_t grid) {
   return f32_wide_dpt<D>() != kF32NarrowDpt && grid * waves < 1024;
 }
 
-template <int D, bool C, int DPT>
+template <int D, bool C, int DPT, int KG>
 void launch_fwd_f32_as(const void* q, const void* k, const void* v, void* o, float* lse,
                        const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
                        float scale, int tmax, void* ws, int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads * kF32Split;
   const int hm = attn_head_major(heads, tmax);
-  hipLaunchKernelGGL((attn_fwd_f32_kernel<D, C, DPT>), dim3((unsigned)grid),
-                     dim3(f32_threads<D, DPT>()), 0,
+  hipLaunchKernelGGL((attn_fwd_f32_kernel<D, C, DPT, KG>), dim3((unsigned)grid),
+                     dim3(f32_threads<D, DPT, KG>()), 0,
                      stream, static_cast<const float*>(q), static_cast<const float*>(k),
                      static_cast<const float*>(v), static_cast<float*>(o), lse,
                      fwd_item_source(ws, cu, batch, total, tmax, heads, D, hm), tmax, hm, heads,
@@ -2521,24 +2560,27 @@ template <int D, bool C>
 void launch_fwd_f32(const void* q, const void* k, const void* v, void* o, float* lse,
                     const int32_t* cu, int batch, int heads, int kv_heads, const int64_t* st,
                     float scale, int tmax, void* ws, int total, hipStream_t stream) {
-  if (f32_use_wide<D>((int64_t)tmax * heads * kF32Split))
-    launch_fwd_f32_as<D, C, f32_wide_dpt<D>()>(q, k, v, o, lse, cu, batch, heads, kv_heads, st,
-                                               scale, tmax, ws, total, stream);
-  else
-    launch_fwd_f32_as<D, C, kF32NarrowDpt>(q, k, v, o, lse, cu, batch, heads, kv_heads, st, scale,
-                                           tmax, ws, total, stream);
+  if constexpr (f32_wide_dpt<D>() != kF32NarrowDpt) {  // (head_dim 256 has no wide form)
+    if (f32_use_wide<D>((int64_t)tmax * heads * kF32Split)) {
+      launch_fwd_f32_as<D, C, f32_wide_dpt<D>(), 2>(q, k, v, o, lse, cu, batch, heads, kv_heads,
+                                                    st, scale, tmax, ws, total, stream);
+      return;
+    }
+  }
+  launch_fwd_f32_as<D, C, kF32NarrowDpt, 1>(q, k, v, o, lse, cu, batch, heads, kv_heads, st, scale,
+                                            tmax, ws, total, stream);
 }
 
 // strides: {dout, q, k, v, o, dq} x {row, head}
-template <int D, bool C, int DPT>
+template <int D, bool C, int DPT, int KG>
 void launch_bwd_dq_f32_as(const void* dout, const void* q, const void* k, const void* v,
                           const void* o, const float* lse, void* dq, float* delta, int heads,
                           int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                           int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * heads * kF32Split;
   const int hm = attn_head_major(heads, tmax);
-  hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, C, DPT>), dim3((unsigned)grid),
-                     dim3(f32_threads<D, DPT>()), 0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
+  hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, C, DPT, KG>), dim3((unsigned)grid),
+                     dim3(f32_threads<D, DPT, KG>()), 0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
                      static_cast<const float*>(k), static_cast<const float*>(v),
                      static_cast<const float*>(o), lse, delta, static_cast<float*>(dq),
                      list_item_source(ws, total, tmax, hm), tmax, hm, heads, heads / kv_heads,
@@ -2552,24 +2594,27 @@ void launch_bwd_dq_f32(const void* dout, const void* q, const void* k, const voi
                        const void* o, const float* lse, void* dq, float* delta, int heads,
                        int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                        int total, hipStream_t stream) {
-  if (f32_use_wide<D>((int64_t)tmax * heads * kF32Split))
-    launch_bwd_dq_f32_as<D, C, f32_wide_dpt<D>()>(dout, q, k, v, o, lse, dq, delta, heads, kv_heads,
-                                                  st, scale, tmax, ws, total, stream);
-  else
-    launch_bwd_dq_f32_as<D, C, kF32NarrowDpt>(dout, q, k, v, o, lse, dq, delta, heads, kv_heads, st,
-                                              scale, tmax, ws, total, stream);
+  if constexpr (f32_wide_dpt<D>() != kF32NarrowDpt) {
+    if (f32_use_wide<D>((int64_t)tmax * heads * kF32Split)) {
+      launch_bwd_dq_f32_as<D, C, f32_wide_dpt<D>(), 2>(dout, q, k, v, o, lse, dq, delta, heads,
+                                                       kv_heads, st, scale, tmax, ws, total, stream);
+      return;
+    }
+  }
+  launch_bwd_dq_f32_as<D, C, kF32NarrowDpt, 1>(dout, q, k, v, o, lse, dq, delta, heads, kv_heads,
+                                               st, scale, tmax, ws, total, stream);
 }
 
 // strides: {dout, q, k, v, dk, dv} x {row, head}; one workgroup per (item, K/V head)
-template <int D, bool C, int DPT>
+template <int D, bool C, int DPT, int KG>
 void launch_bwd_dkv_f32_as(const void* dout, const void* q, const void* k, const void* v,
                            const float* lse, const float* delta, void* dk, void* dv, int heads,
                            int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                            int total, hipStream_t stream) {
   const int64_t grid = (int64_t)tmax * kv_heads * kF32Split;
   const int hm = attn_head_major(kv_heads, tmax);
-  hipLaunchKernelGGL((attn_bwd_dkv_f32_kernel<D, C, DPT>), dim3((unsigned)grid),
-                     dim3(f32_threads<D, DPT>()), 0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
+  hipLaunchKernelGGL((attn_bwd_dkv_f32_kernel<D, C, DPT, KG>), dim3((unsigned)grid),
+                     dim3(f32_threads<D, DPT, KG>()), 0, stream, static_cast<const float*>(dout), static_cast<const float*>(q),
                      static_cast<const float*>(k), static_cast<const float*>(v), lse, delta,
                      static_cast<float*>(dk), static_cast<float*>(dv),
                      list_item_source(ws, total, tmax, hm), tmax, hm, kv_heads,
@@ -2583,12 +2628,19 @@ void launch_bwd_dkv_f32(const void* dout, const void* q, const void* k, const vo
                         const float* lse, const float* delta, void* dk, void* dv, int heads,
                         int kv_heads, const int64_t* st, float scale, int tmax, const void* ws,
                         int total, hipStream_t stream) {
-  if (f32_use_wide<D>((int64_t)tmax * kv_heads * kF32Split))
-    launch_bwd_dkv_f32_as<D, C, f32_wide_dpt<D>()>(dout, q, k, v, lse, delta, dk, dv, heads,
-                                                   kv_heads, st, scale, tmax, ws, total, stream);
-  else
-    launch_bwd_dkv_f32_as<D, C, kF32NarrowDpt>(dout, q, k, v, lse, delta, dk, dv, heads, kv_heads,
-                                               st, scale, tmax, ws, total, stream);
+  if constexpr (f32_wide_dpt<D>() != kF32NarrowDpt) {
+    if (f32_use_wide<D>((int64_t)tmax * kv_heads * kF32Split)) {
+      // one query group at head_dim 128: two would need 1,024 threads of more
+      // than the 128 registers each that allows
+      constexpr int KG = D >= 128 ? 1 : 2;
+      launch_bwd_dkv_f32_as<D, C, f32_wide_dpt<D>(), KG>(dout, q, k, v, lse, delta, dk, dv, heads,
+                                                         kv_heads, st, scale, tmax, ws, total,
+                                                         stream);
+      return;
+    }
+  }
+  launch_bwd_dkv_f32_as<D, C, kF32NarrowDpt, 1>(dout, q, k, v, lse, delta, dk, dv, heads, kv_heads,
+                                                st, scale, tmax, ws, total, stream);
 }
 
 }  // namespace
