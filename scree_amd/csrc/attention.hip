@@ -1922,10 +1922,11 @@ constexpr int kF32Rows = 32;                // keys (forward, dQ) or queries (dK
 // workgroup holds up to 4x the waves, at the price of repeating each row's
 // softmax arithmetic on more lanes).  Both keep every row within 16 lanes.
 // Measured (MI355X, causal): config 1's 1,980 tokens x 4 heads x 32, a
-// narrow grid of 512 waves, run 56 -> 34 us forward and 182 -> 117 us
-// forward + backward in the wide form; 7,168 tokens x 8 heads x 64 (3,776
-// narrow waves) ran 13 % (forward) and 41 % (forward + backward) slower in
-// it, so only launches below one narrow wave per SIMD take it.
+// narrow grid of 512 waves, run 56 -> 30 us forward and 182 -> 100 us
+// forward + backward in the wide form (with its two key groups, below);
+// 7,168 tokens x 8 heads x 64 (3,776 narrow waves) ran 13 % (forward) and
+// 41 % (forward + backward) slower with the wider rows, so only launches
+// below one narrow wave per SIMD take them.
 constexpr int kF32NarrowDpt = 16;
 template <int D>
 constexpr int f32_wide_dpt() {
