@@ -1936,17 +1936,17 @@ template <int D, int DPT>
 constexpr int f32_tpr() {
   return D / DPT;  // lanes per row
 }
-// KG key groups per row (forward, wide form): the row's keys are dealt out
-// to KG groups of TPR lanes, each keeping its own softmax state, merged at
-// the end of the row pass.
-template <int D, int DPT, int KG = 1>
-constexpr int f32_rows() {  // rows per pass
-  return kF32WgRows * f32_tpr<D, DPT>() * KG <= 512 * KG ? kF32WgRows
-                                                         : 512 * KG / (f32_tpr<D, DPT>() * KG);
+// KG groups per row (wide form): the row's keys (forward, dQ) or queries
+// (dK/dV) are dealt out to KG groups of TPR lanes, each keeping its own
+// softmax state or partial sums, merged at the end of the row pass.  Rows
+// per pass: up to 512 threads per group.
+template <int D, int DPT>
+constexpr int f32_rows() {
+  return kF32WgRows * f32_tpr<D, DPT>() <= 512 ? kF32WgRows : 512 / f32_tpr<D, DPT>();
 }
 template <int D, int DPT, int KG = 1>
 constexpr int f32_threads() {
-  return f32_rows<D, DPT, KG>() * f32_tpr<D, DPT>() * KG;
+  return f32_rows<D, DPT>() * f32_tpr<D, DPT>() * KG;
 }
 
 // Sum over the TPR (1 to 16) consecutive lanes of one row, by the DPP steps
@@ -2032,7 +2032,7 @@ __global__ __launch_bounds__((f32_threads<D, DPT, KG>())) void attn_fwd_f32_kern
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ lse, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sq, Strides sk, Strides sv, Strides so, float scale, int total) {
-  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT, KG>(), KT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), KT = kF32Rows;
   static_assert(KT % KG == 0 && (KG == 1 || KG == 2), "one or two key groups");
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
@@ -2140,7 +2140,7 @@ __global__ __launch_bounds__((f32_threads<D, DPT, KG>())) void attn_bwd_dq_f32_k
     float* __restrict__ delta, float* __restrict__ dq, ItemSource src, int tmax, int head_major,
     int heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides so,
     Strides sdq, float scale, int total) {
-  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT, KG>(), KT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), KT = kF32Rows;
   static_assert(KT % KG == 0 && (KG == 1 || KG == 2), "one or two key groups");
   __shared__ __align__(16) float sK[KT * D];
   __shared__ __align__(16) float sV[KT * D];
@@ -2225,7 +2225,7 @@ __global__ __launch_bounds__((f32_threads<D, DPT, KG>())) void attn_bwd_dkv_f32_
     float* __restrict__ dk, float* __restrict__ dv, ItemSource src, int tmax, int head_major,
     int kv_heads, int group, Strides sdo, Strides sq, Strides sk, Strides sv, Strides sdk,
     Strides sdv, float scale, int total) {
-  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT, KG>(), QT = kF32Rows;
+  constexpr int TPR = f32_tpr<D, DPT>(), RPP = f32_rows<D, DPT>(), QT = kF32Rows;
   static_assert(QT % KG == 0 && (KG == 1 || KG == 2), "one or two query groups");
   __shared__ __align__(16) float sQ[QT * D];
   __shared__ __align__(16) float sO[QT * D];  // dO rows
