@@ -324,11 +324,16 @@ def time_norms(cfg, steps, warmup):
     return out
 
 
-def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup):
-    """Calibration: torch's own fused attention (default SDPA dispatch) on a
-    uniform-length batch with the same tokens, causal fp16, forward + backward."""
+def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup, backend=None):
+    """Calibration: torch's own fused attention on a uniform-length batch with
+    the same tokens, causal fp16, forward + backward; ``backend`` None is the
+    default SDPA dispatch (flash attention on this build), else the name of a
+    ``torch.nn.attention.SDPBackend``."""
+    import contextlib
+
     import torch
     import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(5)
@@ -337,8 +342,12 @@ def time_sdpa_reference(heads, head_dim, batch, seqlen, steps, warmup):
     for t in (q, k, v):
         t.requires_grad_(True)
 
+    ctx = (lambda: contextlib.nullcontext()) if backend is None else (
+        lambda: sdpa_kernel(getattr(SDPBackend, backend)))
+
     def step():
-        o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        with ctx():
+            o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         o.backward(do)
 
     for _ in range(warmup):
@@ -744,13 +753,18 @@ def main() -> int:
         uni = workloads.AttnConfig("uniform_16x760_fp16_16x64", [760] * 16, 16, 64, "fp16", True, True)
         ours, _ = time_attention(uni, fp16, args.steps, args.warmup, backward=True)
         ref = time_sdpa_reference(16, 64, 16, 760, args.steps, args.warmup)
+        eff = time_sdpa_reference(16, 64, 16, 760, args.steps, args.warmup, backend="EFFICIENT_ATTENTION")
         secondary["vendor_calibration_uniform_16x760"] = {
             "what": "causal fp16 fwd+bwd, 16 seqs x 760 tokens (12160, as cfg4), 16x64: this "
                     "library's step vs torch.nn.functional.scaled_dot_product_attention (default "
-                    "ROCm dispatch, padded batch of equal lengths) on the same GPU",
+                    "ROCm dispatch, which is flash attention on this build, and the memory-"
+                    "efficient backend; padded batch of equal lengths) on the same GPU",
             "ours_ms": round(ours["ms"], 4), "ours_tflops": round(ours["tflops"], 2),
-            "torch_sdpa_ms": round(ref["ms"], 4), "torch_sdpa_tflops": round(ref["tflops"], 2)}
-        log(f"calibration 16x760: ours {ours['tflops']:.0f} TF/s, torch SDPA {ref['tflops']:.0f} TF/s")
+            "torch_sdpa_ms": round(ref["ms"], 4), "torch_sdpa_tflops": round(ref["tflops"], 2),
+            "torch_sdpa_efficient_ms": round(eff["ms"], 4),
+            "torch_sdpa_efficient_tflops": round(eff["tflops"], 2)}
+        log(f"calibration 16x760: ours {ours['tflops']:.0f} TF/s, torch SDPA {ref['tflops']:.0f} TF/s "
+            f"(efficient backend {eff['tflops']:.0f})")
         gm = time_gemm_calibration()
         secondary["vendor_gemm_fp16_8192"] = {
             "what": "torch.matmul fp16 8192x8192x8192, 200 back-to-back calls after the settle, "
