@@ -29,7 +29,9 @@
  *     and must keep every row 16-byte aligned.  head_dim is 16, 32, 64, 128
  *     or 256 (SCREE_ERR_UNSUPPORTED otherwise); the reference's launcher
  *     takes any power of two (src/scree/kernels/triton/varlen_attention.py:217).  lse and delta are contiguous
- *     (total_tokens, heads) fp32.
+ *     (total_tokens, heads) fp32.  With total_tokens == 0 (every sequence
+ *     empty) the tensor pointers may be NULL, as empty tensors may have no
+ *     storage: the call validates the rest and launches nothing.
  *   - Norm tensors are contiguous (rows, dim); rstd / mean are (rows) fp32.
  */
 #ifndef SCREE_HIP_H

@@ -2327,7 +2327,8 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 int check_tensor(const char* fn, const char* name, const void* p, const int64_t* st, int heads,
                  int head_dim, int64_t total) {
-  if (!p) return set_error(SCREE_ERR_INVALID, "%s: %s is null", fn, name);
+  if (!p)  // an empty tensor (no tokens) may have no storage: nothing will be read or written
+    return total == 0 ? SCREE_OK : set_error(SCREE_ERR_INVALID, "%s: %s is null", fn, name);
   if (!aligned16(p)) return set_error(SCREE_ERR_INVALID, "%s: %s is not 16-byte aligned", fn, name);
   if (st[0] % 8 || st[1] % 8 || st[0] < 0 || st[1] < 0)
     return set_error(SCREE_ERR_INVALID,
@@ -2726,7 +2727,8 @@ static int check_fwd(const char* fn, const void* q, const void* k, const void* v
   if (rc) return rc;
   if ((rc = check_heads(fn, heads, kv_heads))) return rc;
   if (!strides) return set_error(SCREE_ERR_INVALID, "%s: strides is null", fn);
-  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  if (total_tokens > 0 && (!lse || !aligned16(lse)))
+    return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
   const char* names[4] = {"q", "k", "v", "o"};
   const void* ptrs[4] = {q, k, v, o};
   for (int i = 0; i < 4; ++i) {
@@ -2857,8 +2859,9 @@ extern "C" int scree_attn_bwd_dq_gqa(const void* dout, const void* q, const void
                         workspace_bytes);
   if (rc) return rc;
   if ((rc = check_heads(fn, heads, kv_heads))) return rc;
-  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
-  if (!delta || !aligned16(delta))
+  if (total_tokens > 0 && (!lse || !aligned16(lse)))
+    return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  if (total_tokens > 0 && (!delta || !aligned16(delta)))
     return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
   const char* names[6] = {"dout", "q", "k", "v", "o", "dq"};
   const void* ptrs[6] = {dout, q, k, v, o, dq};
@@ -2900,8 +2903,9 @@ extern "C" int scree_attn_bwd_dkv_gqa(const void* dout, const void* q, const voi
                         workspace_bytes);
   if (rc) return rc;
   if ((rc = check_heads(fn, heads, kv_heads))) return rc;
-  if (!lse || !aligned16(lse)) return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
-  if (!delta || !aligned16(delta))
+  if (total_tokens > 0 && (!lse || !aligned16(lse)))
+    return set_error(SCREE_ERR_INVALID, "%s: lse null or unaligned", fn);
+  if (total_tokens > 0 && (!delta || !aligned16(delta)))
     return set_error(SCREE_ERR_INVALID, "%s: delta null or unaligned", fn);
   const char* names[6] = {"dout", "q", "k", "v", "dk", "dv"};
   const void* ptrs[6] = {dout, q, k, v, dk, dv};

@@ -69,6 +69,26 @@ def test_attention_validation_errors():
     assert rc == _ffi.SCREE_ERR_INVALID and "delta" in _err()
 
 
+def test_attention_without_tokens_needs_no_tensors():
+    """No tokens (every sequence empty): empty tensors may have no storage,
+    so null tensor pointers are accepted and nothing is launched."""
+    lib = _ffi.lib()
+    ws = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.c_void_p(ctypes.addressof(ws))
+    null = ctypes.c_void_p(0)
+    strides = _ffi.int64_array([16 * 64, 64] * 8)
+    rc = lib.scree_attn_fwd(null, null, null, null, null, p, 3, 0, 16, 64, strides, 0.125, 1, 1, p,
+                            1 << 16, null)
+    assert rc == _ffi.SCREE_OK, _err()
+    rc = lib.scree_attn_bwd(null, null, null, null, null, null, null, null, null, null, p, 3, 0, 16,
+                            64, strides, 0.125, 1, 1, p, 1 << 16, null)
+    assert rc == _ffi.SCREE_OK, _err()
+    # with tokens the same nulls are rejected
+    rc = lib.scree_attn_fwd(null, null, null, null, null, p, 3, 5, 16, 64, strides, 0.125, 1, 1, p,
+                            1 << 16, null)
+    assert rc == _ffi.SCREE_ERR_INVALID
+
+
 def test_workspace_sizes():
     lib = _ffi.lib()
     # header + two lists of (ceil(N/128) + B) int4 items

@@ -524,3 +524,28 @@ def test_array_level_api_on_device():
     other = scree.pack([randn((n, 2, 64), torch.float16, 1) for n in (6, 76, 130)])
     with pytest.raises(ValueError, match="identical offsets"):
         varlen_attention(q, other, other)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_batch_without_tokens(dtype):
+    """Every sequence empty: empty outputs and gradients, as the reference's
+    torch branch returns (``reference/varlen_attention.py:96-113``), through
+    the launchers, autograd and the Array-level call."""
+    import scree_amd
+    from scree_amd.kernels import varlen_attention
+    from scree_amd.kernels.hip import varlen_attention_hip, varlen_attention_hip_backward
+
+    say(f"case: three empty sequences, H=4 D=64 {dtype}")
+    off, cu = cu_of([0, 0, 0])
+    q, k, v = (torch.empty((0, 4, 64), dtype=dtype, device="cuda") for _ in range(3))
+    if dtype != torch.float32:
+        out, lse = varlen_attention_hip(q, k, v, cu, causal=True, return_lse=True)
+        assert out.shape == (0, 4, 64) and lse.shape == (0, 4)
+        grads = varlen_attention_hip_backward(torch.empty_like(q), q, k, v, out, lse, cu, causal=True)
+        assert all(g.shape == (0, 4, 64) for g in grads)
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    res = varlen_attention(*(scree_amd.Array(values=t, offsets=cu) for t in (qa, ka, va)), causal=True)
+    assert res.values.shape == (0, 4, 64) and res.values.dtype == dtype
+    res.values.sum().backward()
+    torch.cuda.synchronize()
+    assert qa.grad.shape == (0, 4, 64) and ka.grad.shape == (0, 4, 64)
