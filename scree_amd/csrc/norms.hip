@@ -799,7 +799,9 @@ extern "C" int scree_layernorm_fwd(const void* x, const void* weight, const void
 static int validate_bwd(const char* fn, const void* dy, const void* x, const float* rstd, void* dx,
                         bool want_params, int dparam_dtype, int64_t rows, int64_t dim,
                         void* workspace, size_t workspace_bytes) {
-  if (!dy || !x || !rstd || !dx)
+  // with no rows, empty row tensors may have no storage: only the parameter
+  // gradients (sums over no rows: zeros) are written
+  if (rows > 0 && (!dy || !x || !rstd || !dx))
     return set_error(SCREE_ERR_INVALID, "%s: dy, x, rstd and dx must be non-null", fn);
   if (want_params) {
     if (dparam_dtype != SCREE_DTYPE_F32 && dparam_dtype != SCREE_DTYPE_F16 &&
@@ -843,7 +845,7 @@ extern "C" int scree_layernorm_bwd(const void* dy, const void* x, const void* we
   if (rc) return rc;
   if (dweight && !weight) return set_error(SCREE_ERR_INVALID, "%s: dweight requires weight", fn);
   if (rows == 0 && !dweight && !dbias) return SCREE_OK;
-  if (!mean) return set_error(SCREE_ERR_INVALID, "%s: mean must be non-null", fn);
+  if (rows > 0 && !mean) return set_error(SCREE_ERR_INVALID, "%s: mean must be non-null", fn);
   rc = validate_bwd(fn, dy, x, rstd, dx, dweight != nullptr || dbias != nullptr, dparam_dtype, rows,
                     dim, workspace, workspace_bytes);
   if (rc) return rc;

@@ -176,3 +176,25 @@ def test_backward_deterministic():
     torch.cuda.synchronize()
     for a, c in zip(r1, r2):
         assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_zero_rows(dtype):
+    """No rows: empty outputs, and parameter gradients that are sums over no
+    rows, i.e. zeros (not left unwritten)."""
+    from scree_amd.kernels.hip.norms import (layernorm_bwd, layernorm_fwd, rmsnorm_bwd,
+                                             rmsnorm_fwd)
+
+    say(f"case: zero rows, dim 256, {dtype}")
+    x = torch.empty((0, 256), dtype=dtype, device="cuda")
+    w = randn((256,), dtype, 1, scale=0.02, mean=1.0)
+    b = randn((256,), dtype, 2, scale=0.02)
+    y, rstd = rmsnorm_fwd(x, w, 1e-6, True)
+    assert y.shape == (0, 256) and rstd.shape == (0,)
+    dx, dw = rmsnorm_bwd(torch.empty_like(x), x, w, rstd, True, dw_like=w)
+    y2, mean, rstd2 = layernorm_fwd(x, w, b, 1e-6, True)
+    dx2, dw2, db2 = layernorm_bwd(torch.empty_like(x), x, w, mean, rstd2, True, True, p_like=w)
+    torch.cuda.synchronize()
+    assert dx.shape == (0, 256) and dx2.shape == (0, 256) and y2.shape == (0, 256)
+    for g in (dw, dw2, db2):
+        assert g.shape == (256,) and torch.count_nonzero(g).item() == 0
