@@ -198,3 +198,22 @@ def test_zero_rows(dtype):
     assert dx.shape == (0, 256) and dx2.shape == (0, 256) and y2.shape == (0, 256)
     for g in (dw, dw2, db2):
         assert g.shape == (256,) and torch.count_nonzero(g).item() == 0
+
+
+def test_zero_rows_through_the_array_level_calls():
+    import scree_amd
+    from scree_amd.kernels import varlen_layernorm, varlen_rmsnorm, varlen_softmax
+
+    say("case: Array-level norms and softmax on three empty sequences, with autograd")
+    cu = torch.zeros(4, dtype=torch.int32, device="cuda")
+    x = torch.empty((0, 64), dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    w = torch.ones(64, dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    b = torch.zeros(64, dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    arr = scree_amd.Array(values=x, offsets=cu)
+    outs = [varlen_rmsnorm(arr, w), varlen_layernorm(arr, w, b), varlen_softmax(arr)]
+    total = sum(o.values.float().sum() for o in outs)
+    total.backward()
+    torch.cuda.synchronize()
+    assert all(o.values.shape == (0, 64) for o in outs)
+    assert x.grad.shape == (0, 64)
+    assert torch.count_nonzero(w.grad).item() == 0 and torch.count_nonzero(b.grad).item() == 0
