@@ -61,7 +61,7 @@ def test_rmsnorm_fwd_bwd(dtype, shape, with_w):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", SHAPES)
-@pytest.mark.parametrize("params", ["wb", "w", "none"])
+@pytest.mark.parametrize("params", ["wb", "w", "b", "none"])
 def test_layernorm_fwd_bwd(dtype, shape, params):
     from scree_amd.kernels.hip.norms import layernorm_bwd as hip_bwd, layernorm_fwd as hip_fwd
 

@@ -53,7 +53,7 @@ def test_random_rmsnorm(case):
 @pytest.mark.parametrize("case", LN, ids=[f"ln{c[0]}" for c in LN])
 def test_random_layernorm(case):
     _, rows, dim, dtype, flags = case
-    _ln_case(dtype, (rows, dim), params=["wb", "w", "none", "wb"][flags])
+    _ln_case(dtype, (rows, dim), params=["wb", "w", "none", "b"][flags])
 
 
 @pytest.mark.parametrize("case", ADD, ids=[f"add{c[0]}" for c in ADD])
