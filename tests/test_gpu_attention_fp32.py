@@ -143,3 +143,33 @@ def test_fp32_run_to_run_identical():
                              causal=True).values for _ in range(2)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("heads", [4, 40])  # the wide form, then the narrow one
+def test_fp32_strided_views_match_contiguous(heads):
+    """q, k, v as views into one packed (tokens, 3, heads, 64) fp32 buffer, read
+    in place with its strides: the same values as contiguous copies, and the
+    same gradients."""
+    import scree_amd
+    from scree_amd.kernels import varlen_attention
+
+    lengths = [70, 33, 190, 1]
+    say(f"case: fp32 strided qkv views H={heads}")
+    n = sum(lengths)
+    _, cu = cu_of(lengths)
+    qkv = randn((n, 3, heads, 64), torch.float32, 17)
+    do = randn((n, heads, 64), torch.float32, 18)
+
+    def run(q, k, v):
+        qa, ka, va = (t.detach().requires_grad_(True) for t in (q, k, v))
+        out = varlen_attention(*(scree_amd.Array(values=t, offsets=cu) for t in (qa, ka, va)),
+                               causal=True)
+        out.values.backward(do)
+        return out.values.detach(), qa.grad, ka.grad, va.grad
+
+    strided = run(qkv[:, 0], qkv[:, 1], qkv[:, 2])
+    contig = run(qkv[:, 0].contiguous(), qkv[:, 1].contiguous(), qkv[:, 2].contiguous())
+    torch.cuda.synchronize()
+    assert not qkv[:, 0].is_contiguous()
+    for a, b in zip(strided, contig):
+        assert torch.equal(a, b)
