@@ -10,16 +10,17 @@
 // (sequence, column chunk): its 256 threads (512 in the backward) are `ct`
 // column lanes (each owning VEC adjacent columns, one 16-byte vector when the
 // row allows it) times `threads / ct` row lanes that stride over the
-// sequence's rows.  Pass 1 keeps an
-// online (max, sum) per column with one exp per element; the row lanes merge
-// through LDS; pass 2 writes the normalised values with streaming stores.
-// When the sequence has at most kSmCache rows per row lane (checked per
-// workgroup), every thread keeps its rows as loaded in registers: pass 1
-// takes the thread's max and then its sum of exponentials, and pass 2 reads
-// the rows from there, so x is read once.  Longer sequences use the online
-// update and re-read their rows in pass 2 (the tensor is then usually still
-// in the L2 / MALL).  Row lanes merge by a fixed tree: results are
-// deterministic.
+// sequence's rows.  Forward pass 1 finds each column's (max, sum of
+// exponentials); the row lanes merge through LDS; pass 2 writes the
+// normalised values with streaming stores.  Each thread keeps its first
+// kSmCache rows in registers as loaded, takes their max and then their sum,
+// and writes them in pass 2 from there, so a sequence of at most
+// kSmCache * (row lanes) rows reads x once.  Rows past that (long
+// sequences) are streamed first with an online (max, sum), one exp per
+// element, merged into the held rows' result, and re-read in pass 2 (usually
+// from the L2 / MALL).  The backward holds y and dy the same way when the
+// whole sequence fits, else streams every row twice.  Row lanes merge by a
+// fixed tree: results are deterministic.
 // Statistics are fp32 for every input dtype; y has x's dtype.
 
 #include <type_traits>
@@ -32,7 +33,11 @@ namespace {
 constexpr int kSmThreads = 256;        // forward: more, smaller workgroups overlap their phases
 constexpr int kSmThreadsBwd = 512;     // backward: more row lanes, so that held rows cover longer sequences
 constexpr int kUnroll = 4;              // rows per thread per loop trip (loads issued together)
-constexpr int kSmCache = 16;            // forward: rows per thread held in registers between the passes
+// Forward: rows per thread held in registers.  16-bit types hold 8 (80
+// VGPRs, 6 waves per SIMD: measured faster than 16 at 4 waves, 74 -> 70 us
+// bf16 and 91 -> 72 us fp16 at 19,758 x 4,096); fp32 keeps 16 (5 waves).
+template <typename T>
+constexpr int sm_cache() { return sizeof(T) == 4 ? 16 : 8; }
 constexpr int kSmCacheBwd = 10;         // backward (y and dy held): 2 workgroups per CU
 constexpr int64_t kSmMinBlocks = 2048;  // narrow the column lanes until the grid is this big
 constexpr float kLog2eSm = 1.4426950408889634f;
@@ -142,7 +147,15 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
   const int tc = threadIdx.x % ct, tr = threadIdx.x / ct;
   const int64_t col = ((int64_t)chunk * ct + tc) * VEC;
   const bool active = col < features;  // VEC > 1 only when features % VEC == 0
-  const bool cached = end - start <= (int64_t)kSmCache * rs;  // uniform per workgroup
+  // The first kSmCache * rs rows of the sequence are held in registers
+  // (kSmCache per thread).  Rows past them ("excess", only in sequences
+  // longer than that) are streamed first with an online (max, sum), which is
+  // parked in this thread's own LDS merge slots while the held rows load, so
+  // the two never occupy registers together; pass 2 re-reads them.
+  const int64_t len = end - start;
+  constexpr int kSmCache = sm_cache<T>();
+  const int64_t held_rows = (int64_t)kSmCache * rs;
+  const bool excess = len > held_rows;  // uniform per workgroup
 
   float m[VEC], l[VEC];
 #pragma unroll
@@ -151,54 +164,65 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
     l[e] = 0.f;
   }
   Held<T, VEC> held[kSmCache];
+  // rows this thread holds (0 when the sequence is shorter than tr + 1)
+  const int nr = (int)min<int64_t>(kSmCache, max<int64_t>(0, (len - tr + rs - 1) / rs));
   if (active) {
-    if (cached) {
-      // every load in flight before any math; rows past the end stay unread
-      const int nr = (int)min<int64_t>(kSmCache, (end - start - tr + rs - 1) / rs);  // rows held
-#pragma unroll
-      for (int i = 0; i < kSmCache; ++i)
-        if (i < nr) held[i].load(x + (start + tr + (int64_t)i * rs) * features + col);
-      // With the rows at hand, the thread's max first and then the sum of
-      // exponentials against it (fewer instructions than the online update).
-#pragma unroll
-      for (int i = 0; i < kSmCache; i += 2) {
-        if (i >= nr) continue;
-        float a[VEC], b[VEC];
-        held[i].get(a);
-        if (i + 1 < nr)
-          held[i + 1].get(b);
-        else
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) b[e] = a[e];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) m[e] = max3f(m[e], a[e], b[e]);
-      }
-#pragma unroll
-      for (int i = 0; i < kSmCache; ++i) {
-        if (i >= nr) continue;
-        float v[VEC];
-        held[i].get(v);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e)  // m = -inf: every value is -inf, nothing to add
-          l[e] += m[e] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f((v[e] - m[e]) * kLog2eSm);
-      }
-    } else {
-      for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
-        float v[kUnroll][VEC];  // kUnroll rows' loads in flight before any math
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          if (r + u * rs < end) {
-            Vec<T, VEC>::load(x + (r + u * rs) * features + col, v[u]);
-          } else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) v[u][e] = -__builtin_inff();  // a no-op update
-          }
-        }
+    if (excess) {
+      for (int64_t r = start + held_rows + tr; r < end; r += kUnroll * rs) {
+        Held<T, VEC> v[kUnroll];  // kUnroll rows' loads in flight before any math, kept packed
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
+          if (r + u * rs < end) v[u].load(x + (r + u * rs) * features + col);
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) sm_update(m[e], l[e], v[u][e]);
+        for (int u = 0; u < kUnroll; ++u) {
+          if (r + u * rs >= end) continue;
+          float f[VEC];
+          v[u].get(f);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) sm_update(m[e], l[e], f[e]);
+        }
       }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        s_m[threadIdx.x * VEC + e] = m[e];
+        s_l[threadIdx.x * VEC + e] = l[e];
+        m[e] = -__builtin_inff();
+        l[e] = 0.f;
+      }
+    }
+    // the held rows: every load in flight before any math; rows past the
+    // end stay unread
+#pragma unroll
+    for (int i = 0; i < kSmCache; ++i)
+      if (i < nr) held[i].load(x + (start + tr + (int64_t)i * rs) * features + col);
+    // With the rows at hand, the thread's max first and then the sum of
+    // exponentials against it (fewer instructions than the online update).
+#pragma unroll
+    for (int i = 0; i < kSmCache; i += 2) {
+      if (i >= nr) continue;
+      float a[VEC], b[VEC];
+      held[i].get(a);
+      if (i + 1 < nr)
+        held[i + 1].get(b);
+      else
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) b[e] = a[e];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) m[e] = max3f(m[e], a[e], b[e]);
+    }
+#pragma unroll
+    for (int i = 0; i < kSmCache; ++i) {
+      if (i >= nr) continue;
+      float v[VEC];
+      held[i].get(v);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)  // m = -inf: every value is -inf, nothing to add
+        l[e] += m[e] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f((v[e] - m[e]) * kLog2eSm);
+    }
+    if (excess) {  // fold in the streamed rows' (max, sum)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        sm_merge(m[e], l[e], s_m[threadIdx.x * VEC + e], s_l[threadIdx.x * VEC + e]);
     }
   }
   // merge the row lanes of each column: a tree over the (power-of-two) row
@@ -236,31 +260,28 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
     mm[e] = s_m[tc * VEC + e];
     inv[e] = s_l[tc * VEC + e];
   }
-  if (cached) {
 #pragma unroll
-    for (int i = 0; i < kSmCache; ++i) {
-      const int64_t r = start + tr + (int64_t)i * rs;
-      if (r >= end) continue;  // (not break: a fixed trip count keeps the array in registers)
-      float v[VEC];
-      held[i].get(v);
+  for (int i = 0; i < kSmCache; ++i) {
+    if (i >= nr) continue;  // (not break: a fixed trip count keeps the array in registers)
+    float v[VEC];
+    held[i].get(v);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) v[e] = __builtin_amdgcn_exp2f((v[e] - mm[e]) * kLog2eSm) * inv[e];
-      Vec<T, VEC>::store(y + r * features + col, v);
-    }
-    return;
+    for (int e = 0; e < VEC; ++e) v[e] = __builtin_amdgcn_exp2f((v[e] - mm[e]) * kLog2eSm) * inv[e];
+    Vec<T, VEC>::store(y + (start + tr + (int64_t)i * rs) * features + col, v);
   }
-  for (int64_t r = start + tr; r < end; r += kUnroll * rs) {
-    float v[kUnroll][VEC];
+  for (int64_t r = start + held_rows + tr; r < end; r += kUnroll * rs) {
+    Held<T, VEC> v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
-      if (r + u * rs < end) Vec<T, VEC>::load(x + (r + u * rs) * features + col, v[u]);
+      if (r + u * rs < end) v[u].load(x + (r + u * rs) * features + col);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      if (r + u * rs >= end) break;
+      if (r + u * rs >= end) continue;
+      float f[VEC];
+      v[u].get(f);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e)
-        v[u][e] = __builtin_amdgcn_exp2f((v[u][e] - mm[e]) * kLog2eSm) * inv[e];
-      Vec<T, VEC>::store(y + (r + u * rs) * features + col, v[u]);
+      for (int e = 0; e < VEC; ++e) f[e] = __builtin_amdgcn_exp2f((f[e] - mm[e]) * kLog2eSm) * inv[e];
+      Vec<T, VEC>::store(y + (r + u * rs) * features + col, f);
     }
   }
 }
@@ -439,7 +460,7 @@ int launch_softmax(const void* x, void* y, const int32_t* cu, int batch, int64_t
                    int64_t features, hipStream_t stream) {
   constexpr int V = 16 / sizeof(T);
   const SmShape sh = sm_shape<T>(features, aligned16(x) && aligned16(y), batch, total,
-                                 kSmThreads, kSmCache, 4);
+                                 kSmThreads, sm_cache<T>(), 4);
   if ((int64_t)batch * sh.chunks > 0x7fffffff)
     return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: grid too large");
   const dim3 grid((unsigned)(batch * sh.chunks));

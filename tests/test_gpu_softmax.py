@@ -51,8 +51,9 @@ def test_softmax_shapes(dtype, features):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_register_capacity_boundary(dtype):
     """64 features: the forward narrows to 4 column lanes (half-line chunks,
-    paired on one XCD), whose 64 row lanes hold 16 rows each in registers
-    (1,024 rows; 1,025 are re-read); the backward stops at 8 column lanes,
+    paired on one XCD), whose 64 row lanes hold 8 bf16 rows each in registers
+    (512 rows; from 513 on, the rows past 512 are streamed first and re-read)
+    or 16 fp32 rows (1,024; 1,025); the backward stops at 8 column lanes,
     whose 64 row lanes hold 10 rows of y and dy (640 rows; 641 are re-read)."""
     _run([512, 513, 640, 641, 1024, 1025, 3], (64,), dtype, seed=11)
 
@@ -84,8 +85,10 @@ def test_non_finite_inputs_match_two_pass_semantics(length):
     """NaN, +inf and all -inf columns give what the max-subtracted two-pass
     formula (the oracle, pinned to torch.softmax) gives: NaN throughout the
     affected column.  5000 rows of 8 fp32 columns exceed what the forward keeps
-    in registers (16 rows per row lane, 128 row lanes), so the online update
-    and the row-lane merge see the non-finite values; 300 rows stay cached."""
+    in registers (16 rows per row lane, 128 row lanes: 2,048 rows), so the
+    online update of the rows past those, its merge with the held rows' result
+    and the row-lane merge all see non-finite values (column 3 has a +inf on
+    each side); 300 rows stay held."""
     from scree_amd.kernels.hip import varlen_softmax_hip
 
     say(f"case: non-finite softmax length {length}")
