@@ -30,14 +30,21 @@
 namespace scree {
 namespace {
 
-constexpr int kSmThreads = 256;        // forward: more, smaller workgroups overlap their phases
 constexpr int kSmThreadsBwd = 512;     // backward: more row lanes, so that held rows cover longer sequences
 constexpr int kUnroll = 4;              // rows per thread per loop trip (loads issued together)
-// Forward: rows per thread held in registers.  16-bit types hold 8 (80
-// VGPRs, 6 waves per SIMD: measured faster than 16 at 4 waves, 74 -> 70 us
-// bf16 and 91 -> 72 us fp16 at 19,758 x 4,096); fp32 keeps 16 (5 waves).
+// Forward: rows per thread held in registers, 8 for every dtype: 80
+// registers for 16-bit types (6 waves per SIMD; 16 rows took 123-151, 3-4
+// waves, and ran 74 / 91 us bf16 / fp16 against 70 / 72 at 19,758 x 4,096),
+// 64 for fp32 (8 waves; 131 us against 140 with 16 rows).
+constexpr int kSmCache = 8;
+// Forward threads per workgroup and the fewest column lanes it narrows to:
+// 256 and 4 for 16-bit types (64-byte row segments, more and smaller
+// workgroups overlapping their phases); 512 and 8 for fp32 (full 128-byte
+// segments: 140 against 169 us at 256 / 4, config-2 shape in fp32).
 template <typename T>
-constexpr int sm_cache() { return sizeof(T) == 4 ? 16 : 8; }
+constexpr int sm_threads() { return sizeof(T) == 4 ? 512 : 256; }
+template <typename T>
+constexpr int sm_min_ct() { return sizeof(T) == 4 ? 8 : 4; }
 constexpr int kSmCacheBwd = 10;         // backward (y and dy held): 2 workgroups per CU
 constexpr int64_t kSmMinBlocks = 2048;  // narrow the column lanes until the grid is this big
 constexpr float kLog2eSm = 1.4426950408889634f;
@@ -133,9 +140,10 @@ __device__ __forceinline__ int sm_block(bool half_lines) {
 }
 
 template <typename T, int VEC>
-__global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
+__global__ __launch_bounds__(sm_threads<T>()) void varlen_softmax_kernel(
     const T* __restrict__ x, T* __restrict__ y, const int32_t* __restrict__ cu, int64_t total,
     int64_t features, int ct, int chunks) {
+  constexpr int kSmThreads = sm_threads<T>();
   __shared__ float s_m[kSmThreads * VEC];
   __shared__ float s_l[kSmThreads * VEC];
   const int bsel = sm_block(ct * VEC * (int)sizeof(T) < 128);
@@ -153,7 +161,6 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
   // parked in this thread's own LDS merge slots while the held rows load, so
   // the two never occupy registers together; pass 2 re-reads them.
   const int64_t len = end - start;
-  constexpr int kSmCache = sm_cache<T>();
   const int64_t held_rows = (int64_t)kSmCache * rs;
   const bool excess = len > held_rows;  // uniform per workgroup
 
@@ -210,14 +217,20 @@ __global__ __launch_bounds__(kSmThreads) void varlen_softmax_kernel(
 #pragma unroll
       for (int e = 0; e < VEC; ++e) m[e] = max3f(m[e], a[e], b[e]);
     }
+    // The sum against mr = m, or 0 where m = -inf (every held value -inf or
+    // NaN, as v_max3 skips NaN): -inf then adds exp2(-inf) = 0 and a NaN adds
+    // NaN, as in the two-pass formula, where a guard on m = -inf would drop
+    // the NaN.
+    float mr[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) mr[e] = m[e] == -__builtin_inff() ? 0.f : m[e];
 #pragma unroll
     for (int i = 0; i < kSmCache; ++i) {
       if (i >= nr) continue;
       float v[VEC];
       held[i].get(v);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e)  // m = -inf: every value is -inf, nothing to add
-        l[e] += m[e] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f((v[e] - m[e]) * kLog2eSm);
+      for (int e = 0; e < VEC; ++e) l[e] += __builtin_amdgcn_exp2f((v[e] - mr[e]) * kLog2eSm);
     }
     if (excess) {  // fold in the streamed rows' (max, sum)
 #pragma unroll
@@ -460,16 +473,16 @@ int launch_softmax(const void* x, void* y, const int32_t* cu, int batch, int64_t
                    int64_t features, hipStream_t stream) {
   constexpr int V = 16 / sizeof(T);
   const SmShape sh = sm_shape<T>(features, aligned16(x) && aligned16(y), batch, total,
-                                 kSmThreads, sm_cache<T>(), 4);
+                                 sm_threads<T>(), kSmCache, sm_min_ct<T>());
   if ((int64_t)batch * sh.chunks > 0x7fffffff)
     return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: grid too large");
   const dim3 grid((unsigned)(batch * sh.chunks));
   if (sh.vec)
-    hipLaunchKernelGGL((varlen_softmax_kernel<T, V>), grid, dim3(kSmThreads), 0, stream,
+    hipLaunchKernelGGL((varlen_softmax_kernel<T, V>), grid, dim3(sm_threads<T>()), 0, stream,
                        static_cast<const T*>(x), static_cast<T*>(y), cu, total, features, sh.ct,
                        (int)sh.chunks);
   else
-    hipLaunchKernelGGL((varlen_softmax_kernel<T, 1>), grid, dim3(kSmThreads), 0, stream,
+    hipLaunchKernelGGL((varlen_softmax_kernel<T, 1>), grid, dim3(sm_threads<T>()), 0, stream,
                        static_cast<const T*>(x), static_cast<T*>(y), cu, total, features, sh.ct,
                        (int)sh.chunks);
   return check_launch("scree_varlen_softmax");

@@ -50,11 +50,12 @@ def test_softmax_shapes(dtype, features):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_register_capacity_boundary(dtype):
-    """64 features: the forward narrows to 4 column lanes (half-line chunks,
-    paired on one XCD), whose 64 row lanes hold 8 bf16 rows each in registers
-    (512 rows; from 513 on, the rows past 512 are streamed first and re-read)
-    or 16 fp32 rows (1,024; 1,025); the backward stops at 8 column lanes,
-    whose 64 row lanes hold 10 rows of y and dy (640 rows; 641 are re-read)."""
+    """64 features: the bf16 forward narrows to 4 column lanes (half-line
+    chunks, paired on one XCD) of 256-thread workgroups and the fp32 forward
+    to 8 lanes (full lines) of 512 threads; either way 64 row lanes hold 8
+    rows each in registers (512 rows; from 513 on, the rows past 512 are
+    streamed first and re-read).  The backward stops at 8 column lanes, whose
+    64 row lanes hold 10 rows of y and dy (640 rows; 641 are re-read)."""
     _run([512, 513, 640, 641, 1024, 1025, 3], (64,), dtype, seed=11)
 
 
@@ -80,25 +81,27 @@ def test_rows_sum_to_one_and_masked_entries():
     assert torch.isnan(torch.softmax(x[10:11].cpu(), dim=0)).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("length", [300, 5000])
-def test_non_finite_inputs_match_two_pass_semantics(length):
+def test_non_finite_inputs_match_two_pass_semantics(length, dtype):
     """NaN, +inf and all -inf columns give what the max-subtracted two-pass
     formula (the oracle, pinned to torch.softmax) gives: NaN throughout the
     affected column.  5000 rows of 8 fp32 columns exceed what the forward keeps
-    in registers (16 rows per row lane, 128 row lanes: 2,048 rows), so the
-    online update of the rows past those, its merge with the held rows' result
-    and the row-lane merge all see non-finite values (column 3 has a +inf on
-    each side); 300 rows stay held."""
+    in registers (8 rows per row lane, 256 row lanes: 2,048 rows, in fp32
+    and in bf16), so the online update of the rows past those, its merge
+    with the held rows' result and the row-lane merge all see non-finite
+    values (column 3 has a +inf on each side: rows 5 and length - 3); 300
+    rows stay held."""
     from scree_amd.kernels.hip import varlen_softmax_hip
 
-    say(f"case: non-finite softmax length {length}")
+    say(f"case: non-finite softmax length {length} {dtype}")
     lengths = [length, 7]
     off, cu = cu_of(lengths)
-    x = randn((sum(lengths), 8), torch.float32, 31)
+    x = randn((sum(lengths), 8), dtype, 31)
     x[length // 3, 1] = float("nan")
     x[length - 2, 2] = float("inf")
     x[5, 3] = float("inf")
-    x[length // 2, 3] = float("inf")                  # two +inf in one column
+    x[length - 3, 3] = float("inf")                   # two +inf in one column
     x[:length, 4] = float("-inf")                      # a column with no finite value
     x[7, 5] = float("nan")
     x[:length, 5][x[:length, 5] == x[:length, 5]] = float("-inf")  # only -inf and one NaN
@@ -110,9 +113,35 @@ def test_non_finite_inputs_match_two_pass_semantics(length):
     got = np64(y)
     np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
     fin = ~np.isnan(want)
-    check_close("y (finite entries)", got[fin], want[fin], 1e-5)
+    u = 0.0 if dtype == torch.float32 else UNIT[dtype]
+    check_close("y (finite entries)", got[fin], want[fin], ATOL[dtype], extra=np.abs(want[fin]), unit=u)
     assert np.isnan(got[:length, 1:6]).all()
     assert got[length - 1, 6] == 1.0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_nan_held_alone_in_its_row_lane(dtype):
+    """A NaN among finite values of a short sequence: every row lane holds at
+    most one row, so the lane holding the NaN has no other value.  Its max
+    (v_max3 skips NaN) is -inf, and its sum must still carry the NaN so that
+    the column is NaN throughout, as in the two-pass formula."""
+    from scree_amd.kernels.hip import varlen_softmax_hip
+
+    say(f"case: NaN alone in its row lane {dtype}")
+    lengths = [10, 3, 40]
+    off, cu = cu_of(lengths)
+    x = randn((sum(lengths), 8), dtype, 41)
+    x[4, 1] = float("nan")           # sequence 0
+    x[13 + 20, 6] = float("nan")     # sequence 2
+    y = varlen_softmax_hip(x, cu)
+    torch.cuda.synchronize()
+    want = varlen_softmax(np64(x), off)
+    got = np64(y)
+    assert np.isnan(want[0:10, 1]).all() and np.isnan(want[13:53, 6]).all()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    u = 0.0 if dtype == torch.float32 else UNIT[dtype]
+    check_close("y (finite entries)", got[fin], want[fin], ATOL[dtype], extra=np.abs(want[fin]), unit=u)
 
 
 def test_non_contiguous_view():
