@@ -24,7 +24,8 @@ fixed H100 length list, config 4 with grouped-query attention (16 query heads
 on 4 K/V heads), config 5 (bf16, 32x128) forward+backward, config 2
 RMSNorm / LayerNorm / fused add + RMSNorm forward and backward GB/s, varlen
 softmax forward and backward and packed <-> padded conversions GB/s at the
-config-2 shape, the reference's 27-shape sweep (head_dim x heads x mean
+config-2 shape (each op cycling over three input sets, so that its input is
+not still cached from the previous call), the reference's 27-shape sweep (head_dim x heads x mean
 length, fp16 causal, forward and forward+backward), torch's own SDPA on the same GPU for calibration (uniform
 lengths with cfg4's token count), the vendor GEMM's fp16 rate on random and
 on constant operands (the clock this GPU holds on real data), config 4
@@ -74,6 +75,10 @@ def _settle(fn) -> None:
         for _ in range(8):
             fn()
         torch.cuda.synchronize()
+
+
+# Input sets the HBM-bound timings cycle over (3 x 162 MB per activation).
+NROT = 3
 
 
 def _events_time(fn, reps: int) -> float:
@@ -252,73 +257,88 @@ def time_attention(cfg, dtype, steps, warmup, backward, per_kernel=False, kv_hea
 
 
 def time_norms(cfg, steps, warmup):
+    """Config-2 norms, softmax and packed <-> padded ops, bf16.  Every case
+    cycles over NROT sets of inputs (each activation 162 MB, so one cycle
+    reads more than the GPU's 256 MB last-level cache): a kernel that reads
+    with ordinary loads would otherwise find its input still cached from the
+    previous call and be credited with more than HBM bandwidth (measured:
+    the softmax forward 68 us on one repeated input against 94 us cycling)."""
     import torch
 
     from scree_amd import workloads
     from scree_amd.kernels.hip import norms as Nm
+    from scree_amd.kernels.hip import padding as Pd
+    from scree_amd.kernels.hip import softmax as Sm
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(2)
     rows, dim = cfg.total, cfg.hidden
     dt = torch.bfloat16
-    x = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
     w = (1 + 0.02 * torch.randn(dim, device=dev, generator=g)).to(dt)
     b = (0.02 * torch.randn(dim, device=dev, generator=g)).to(dt)
-    dy = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
-    _, rstd = Nm.rmsnorm_fwd(x, w, cfg.eps, True)
-    _, mean, lrstd = Nm.layernorm_fwd(x, w, b, cfg.eps, True)
+    off = torch.zeros(len(cfg.lengths) + 1, dtype=torch.int32)
+    off[1:] = torch.cumsum(torch.tensor(cfg.lengths, dtype=torch.int64), 0).to(torch.int32)
+    cu = off.to(dev)
+    max_len = max(cfg.lengths)
+    sets = []
+    for _ in range(NROT):
+        x = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+        dy = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+        r = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+        dh = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
+        _, rstd = Nm.rmsnorm_fwd(x, w, cfg.eps, True)
+        _, mean, lrstd = Nm.layernorm_fwd(x, w, b, cfg.eps, True)
+        h, _, hrstd = Nm.add_rmsnorm_fwd(x, r, w, cfg.eps, True)
+        ys = Sm.softmax_fwd(x, cu)
+        padded, pmask = Pd.to_padded_hip(x, cu, max_len=max_len)
+        sets.append(dict(x=x, dy=dy, r=r, dh=dh, rstd=rstd, mean=mean, lrstd=lrstd, h=h, hrstd=hrstd,
+                         ys=ys, padded=padded, pmask=pmask))
     fb = workloads.norm_fwd_bytes(rows, dim, 2, False)
     bb = workloads.norm_bwd_bytes(rows, dim, 2, False)
     lfb = workloads.norm_fwd_bytes(rows, dim, 2, True)
     lbb = workloads.norm_bwd_bytes(rows, dim, 2, True)
-    cases = {
-        "rmsnorm_fwd": (lambda: Nm.rmsnorm_fwd(x, w, cfg.eps, True), fb),
-        "rmsnorm_bwd": (lambda: Nm.rmsnorm_bwd(dy, x, w, rstd, True, dw_like=w), bb),
-        "layernorm_fwd": (lambda: Nm.layernorm_fwd(x, w, b, cfg.eps, True), lfb),
-        "layernorm_bwd": (lambda: Nm.layernorm_bwd(dy, x, w, mean, lrstd, True, True, p_like=w), lbb),
-    }
     # fused residual add + RMSNorm: reads x, r (and w), writes h, y; backward
     # reads dy, dh, h (and w), writes dx (and dw)
-    r = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
-    dh = torch.randn(rows, dim, device=dev, dtype=dt, generator=g)
-    h, _, hrstd = Nm.add_rmsnorm_fwd(x, r, w, cfg.eps, True)
     afb = 4.0 * 2 * rows * dim + 2 * dim
     abb = 4.0 * 2 * rows * dim + 2 * 2 * dim
-    cases["add_rmsnorm_fwd"] = (lambda: Nm.add_rmsnorm_fwd(x, r, w, cfg.eps, True), afb)
-    cases["add_rmsnorm_bwd"] = (lambda: Nm.add_rmsnorm_bwd(dy, dh, h, w, hrstd, True, dw_like=w), abb)
-    # the two steps it replaces (torch add, then this library's RMSNorm), same algorithmic bytes
-    cases["unfused_add_then_rmsnorm_fwd"] = (lambda: Nm.rmsnorm_fwd(x + r, w, cfg.eps, True), afb)
-    y = torch.empty_like(x)
-    cases["device_copy_same_bytes"] = (lambda: y.copy_(x), 2.0 * x.numel() * x.element_size())
-    # varlen softmax along the ragged axis at the same shape (x: 19758 x 4096 bf16)
-    from scree_amd.kernels.hip import softmax as Sm
-
-    off = torch.zeros(len(cfg.lengths) + 1, dtype=torch.int32)
-    off[1:] = torch.cumsum(torch.tensor(cfg.lengths, dtype=torch.int64), 0).to(torch.int32)
-    cu = off.to(dev)
-    ys = Sm.softmax_fwd(x, cu)
-    nb = x.numel() * x.element_size()
-    cases["varlen_softmax_fwd"] = (lambda: Sm.softmax_fwd(x, cu, ys), 2.0 * nb)
-    cases["varlen_softmax_bwd"] = (lambda: Sm.softmax_bwd(ys, dy, cu), 3.0 * nb)
-    # packed <-> padded at the same shape: (64, 829, 4096) bf16 padded batch
-    from scree_amd.kernels.hip import padding as Pd
-
-    max_len = max(cfg.lengths)
-    padded, pmask = Pd.to_padded_hip(x, cu, max_len=max_len)
-    row = dim * x.element_size()
+    y = torch.empty(rows, dim, device=dev, dtype=dt)
+    nb = rows * dim * 2
+    row = dim * 2
     pad_rows = len(cfg.lengths) * max_len
-    cases["to_padded"] = (lambda: Pd.to_padded_hip(x, cu, max_len=max_len),
-                          rows * row + pad_rows * (row + 1))
-    cases["from_padded_user_call"] = (lambda: Pd.from_padded_hip(padded, pmask),
-                                      pad_rows + 2.0 * rows * row)
-    # the same call given the token count (no host read of the device total)
-    cases["from_padded_given_total"] = (lambda: Pd.from_padded_hip(padded, pmask, total=rows),
-                                        pad_rows + 2.0 * rows * row)
+    eps = cfg.eps
+    cases = {
+        "rmsnorm_fwd": (lambda s: Nm.rmsnorm_fwd(s["x"], w, eps, True), fb),
+        "rmsnorm_bwd": (lambda s: Nm.rmsnorm_bwd(s["dy"], s["x"], w, s["rstd"], True, dw_like=w), bb),
+        "layernorm_fwd": (lambda s: Nm.layernorm_fwd(s["x"], w, b, eps, True), lfb),
+        "layernorm_bwd": (lambda s: Nm.layernorm_bwd(s["dy"], s["x"], w, s["mean"], s["lrstd"], True, True,
+                                                     p_like=w), lbb),
+        "add_rmsnorm_fwd": (lambda s: Nm.add_rmsnorm_fwd(s["x"], s["r"], w, eps, True), afb),
+        "add_rmsnorm_bwd": (lambda s: Nm.add_rmsnorm_bwd(s["dy"], s["dh"], s["h"], w, s["hrstd"], True,
+                                                         dw_like=w), abb),
+        # the two steps it replaces (torch add, then this library's RMSNorm), same algorithmic bytes
+        "unfused_add_then_rmsnorm_fwd": (lambda s: Nm.rmsnorm_fwd(s["x"] + s["r"], w, eps, True), afb),
+        "device_copy_same_bytes": (lambda s: y.copy_(s["x"]), 2.0 * nb),
+        # varlen softmax along the ragged axis at the same shape (x: 19758 x 4096 bf16)
+        "varlen_softmax_fwd": (lambda s: Sm.softmax_fwd(s["x"], cu, s["ys"]), 2.0 * nb),
+        "varlen_softmax_bwd": (lambda s: Sm.softmax_bwd(s["ys"], s["dy"], cu), 3.0 * nb),
+        # packed <-> padded at the same shape: (64, 829, 4096) bf16 padded batch
+        "to_padded": (lambda s: Pd.to_padded_hip(s["x"], cu, max_len=max_len), rows * row + pad_rows * (row + 1)),
+        "from_padded_user_call": (lambda s: Pd.from_padded_hip(s["padded"], s["pmask"]), pad_rows + 2.0 * rows * row),
+        # the same call given the token count (no host read of the device total)
+        "from_padded_given_total": (lambda s: Pd.from_padded_hip(s["padded"], s["pmask"], total=rows),
+                                    pad_rows + 2.0 * rows * row),
+    }
     out = {}
     for name, (fn, nbytes) in cases.items():
+        it = [0]
+
+        def step(fn=fn, it=it):
+            fn(sets[it[0] % NROT])
+            it[0] += 1
+
         for _ in range(warmup):
-            fn()
-        ms = _events_time(fn, steps)
+            step()
+        ms = _events_time(step, steps)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"ms": ms, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS, "bytes": nbytes}
     return out

@@ -39,10 +39,11 @@ struct Unit<1> {
   typedef uint8_t type;
 };
 
-// Streaming (non-temporal) stores: every output byte is written once, and
-// not allocating it in the caches took to_padded from 112 to 80 us and
-// from_padded from 60 to 55 us at the config-2 shape (19,758 x 4,096 bf16
-// into 64 x 829 rows); non-temporal loads as well were slower (110 / 62).
+// Streaming (non-temporal) stores for to_padded's output (every byte written
+// once): config-2 shape (19,758 x 4,096 bf16 into 64 x 829 rows) 112 -> 107 us
+// with inputs not in the caches.  from_padded keeps plain stores: with them
+// it ran 62 us against 67 from cold inputs (the non-temporal form was faster,
+// 55 against 60 us, only when its input was still cached from the last call).
 template <typename UT>
 __device__ __forceinline__ void st_nt(UT* p, UT v) { __builtin_nontemporal_store(v, p); }
 template <>
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(kPadThreads) void from_padded_kernel(
     if (t >= len) continue;
     const UT* src = reinterpret_cast<const UT*>(padded + row * upr * U);
     UT* dst = reinterpret_cast<UT*>(values + (start + t) * upr * U);
-    for (int64_t c = lane; c < upr; c += tpr) st_nt(dst + c, src[c]);
+    for (int64_t c = lane; c < upr; c += tpr) dst[c] = src[c];
   }
 }
 

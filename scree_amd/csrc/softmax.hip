@@ -37,14 +37,13 @@ constexpr int kUnroll = 4;              // rows per thread per loop trip (loads 
 // waves, and ran 74 / 91 us bf16 / fp16 against 70 / 72 at 19,758 x 4,096),
 // 64 for fp32 (8 waves; 131 us against 140 with 16 rows).
 constexpr int kSmCache = 8;
-// Forward threads per workgroup and the fewest column lanes it narrows to:
-// 256 and 4 for 16-bit types (64-byte row segments, more and smaller
-// workgroups overlapping their phases); 512 and 8 for fp32 (full 128-byte
-// segments: 140 against 169 us at 256 / 4, config-2 shape in fp32).
-template <typename T>
-constexpr int sm_threads() { return sizeof(T) == 4 ? 512 : 256; }
-template <typename T>
-constexpr int sm_min_ct() { return sizeof(T) == 4 ? 8 : 4; }
+// Forward: 512 threads per workgroup, narrowing to no fewer than 8 column
+// lanes (128-byte row segments, whole cache lines).  With inputs not already
+// cached (each call reading fresh data), 4 lanes of 256 threads took 94.5 us
+// at the config-2 shape in bf16 against 77.7 us (the same 69 us either way
+// when the input was still cached from the previous call); fp32 169 -> 140.
+constexpr int kSmThreadsFwd = 512;
+constexpr int kSmMinCtFwd = 8;
 constexpr int kSmCacheBwd = 10;         // backward (y and dy held): 2 workgroups per CU
 constexpr int64_t kSmMinBlocks = 2048;  // narrow the column lanes until the grid is this big
 constexpr float kLog2eSm = 1.4426950408889634f;
@@ -140,10 +139,10 @@ __device__ __forceinline__ int sm_block(bool half_lines) {
 }
 
 template <typename T, int VEC>
-__global__ __launch_bounds__(sm_threads<T>()) void varlen_softmax_kernel(
+__global__ __launch_bounds__(kSmThreadsFwd) void varlen_softmax_kernel(
     const T* __restrict__ x, T* __restrict__ y, const int32_t* __restrict__ cu, int64_t total,
     int64_t features, int ct, int chunks) {
-  constexpr int kSmThreads = sm_threads<T>();
+  constexpr int kSmThreads = kSmThreadsFwd;
   __shared__ float s_m[kSmThreads * VEC];
   __shared__ float s_l[kSmThreads * VEC];
   const int bsel = sm_block(ct * VEC * (int)sizeof(T) < 128);
@@ -473,16 +472,16 @@ int launch_softmax(const void* x, void* y, const int32_t* cu, int batch, int64_t
                    int64_t features, hipStream_t stream) {
   constexpr int V = 16 / sizeof(T);
   const SmShape sh = sm_shape<T>(features, aligned16(x) && aligned16(y), batch, total,
-                                 sm_threads<T>(), kSmCache, sm_min_ct<T>());
+                                 kSmThreadsFwd, kSmCache, kSmMinCtFwd);
   if ((int64_t)batch * sh.chunks > 0x7fffffff)
     return set_error(SCREE_ERR_INVALID, "scree_varlen_softmax: grid too large");
   const dim3 grid((unsigned)(batch * sh.chunks));
   if (sh.vec)
-    hipLaunchKernelGGL((varlen_softmax_kernel<T, V>), grid, dim3(sm_threads<T>()), 0, stream,
+    hipLaunchKernelGGL((varlen_softmax_kernel<T, V>), grid, dim3(kSmThreadsFwd), 0, stream,
                        static_cast<const T*>(x), static_cast<T*>(y), cu, total, features, sh.ct,
                        (int)sh.chunks);
   else
-    hipLaunchKernelGGL((varlen_softmax_kernel<T, 1>), grid, dim3(sm_threads<T>()), 0, stream,
+    hipLaunchKernelGGL((varlen_softmax_kernel<T, 1>), grid, dim3(kSmThreadsFwd), 0, stream,
                        static_cast<const T*>(x), static_cast<T*>(y), cu, total, features, sh.ct,
                        (int)sh.chunks);
   return check_launch("scree_varlen_softmax");

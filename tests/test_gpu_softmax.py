@@ -50,12 +50,11 @@ def test_softmax_shapes(dtype, features):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_register_capacity_boundary(dtype):
-    """64 features: the bf16 forward narrows to 4 column lanes (half-line
-    chunks, paired on one XCD) of 256-thread workgroups and the fp32 forward
-    to 8 lanes (full lines) of 512 threads; either way 64 row lanes hold 8
-    rows each in registers (512 rows; from 513 on, the rows past 512 are
-    streamed first and re-read).  The backward stops at 8 column lanes, whose
-    64 row lanes hold 10 rows of y and dy (640 rows; 641 are re-read)."""
+    """64 features: the forward narrows to 8 column lanes (full 128-byte
+    lines) of 512 threads, whose 64 row lanes hold 8 rows each in registers
+    (512 rows; from 513 on, the rows past 512 are streamed first and
+    re-read).  The backward stops at 8 column lanes too, whose 64 row lanes
+    hold 10 rows of y and dy (640 rows; 641 are re-read)."""
     _run([512, 513, 640, 641, 1024, 1025, 3], (64,), dtype, seed=11)
 
 
@@ -87,11 +86,12 @@ def test_non_finite_inputs_match_two_pass_semantics(length, dtype):
     """NaN, +inf and all -inf columns give what the max-subtracted two-pass
     formula (the oracle, pinned to torch.softmax) gives: NaN throughout the
     affected column.  5000 rows of 8 fp32 columns exceed what the forward keeps
-    in registers (8 rows per row lane, 256 row lanes: 2,048 rows, in fp32
-    and in bf16), so the online update of the rows past those, its merge
-    with the held rows' result and the row-lane merge all see non-finite
-    values (column 3 has a +inf on each side: rows 5 and length - 3); 300
-    rows stay held."""
+    in registers (8 rows per row lane: 2,048 rows in fp32, whose 8 columns
+    are two 16-byte vectors, 256 row lanes; 4,096 in bf16, one vector, 512
+    row lanes), so the online update of the rows past those, its merge with
+    the held rows' result and the row-lane merge all see non-finite values
+    (column 3 has a +inf on each side: rows 5 and length - 3); 300 rows stay
+    held."""
     from scree_amd.kernels.hip import varlen_softmax_hip
 
     say(f"case: non-finite softmax length {length} {dtype}")
